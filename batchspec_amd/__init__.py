@@ -1,0 +1,34 @@
+"""batchspec_amd — MI355X (gfx950) speculative-verification hot path for BatchSpec.
+
+Drop-in names for the FlashInfer entry points BatchSpec calls on its verify path:
+
+* ``BatchPrefillWithPagedKVCacheWrapper``  (plan/run; paged-KV verify attention)
+* ``get_seq_lens``, ``get_batch_indices_positions``, ``append_paged_kv_cache``
+  (paged KV append) and ``StandardKVCache``
+* ``sampling.chain_speculative_sampling``, ``sampling.softmax`` and the fused
+  ``evaluate_posterior`` (acceptance)
+
+All compute runs in ``libbsx.so`` (hand-written HIP for gfx950, C ABI in
+``include/bsx.h``); the Python layer only validates, plans and launches.
+"""
+from .attention import BatchPrefillWithPagedKVCacheWrapper
+from .page import (StandardKVCache, append_kv, append_paged_kv_cache,
+                   get_batch_indices_positions, get_seq_lens)
+from .page_table import PageManager, PageTable
+from .posterior import PosteriorMixin, evaluate_posterior
+from . import masks, sampling
+
+__all__ = [
+    "BatchPrefillWithPagedKVCacheWrapper",
+    "StandardKVCache",
+    "append_kv",
+    "append_paged_kv_cache",
+    "get_batch_indices_positions",
+    "get_seq_lens",
+    "PageManager",
+    "PageTable",
+    "PosteriorMixin",
+    "evaluate_posterior",
+    "masks",
+    "sampling",
+]

@@ -1,0 +1,140 @@
+"""ctypes binding of the C ABI in ``include/bsx.h`` (``batchspec_amd/libbsx.so``).
+
+The library is the only compute path of this package: nothing here falls back to
+PyTorch or to a CPU implementation.  If the shared library has not been built,
+importing the ops raises immediately with the build command to run.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_uint8, c_uint32, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(os.environ.get("BSX_LIB", Path(__file__).resolve().parent / "libbsx.so"))
+
+BSX_OK = 0
+BSX_ERR_INVALID = -1
+BSX_ERR_CAPACITY = -2
+BSX_ERR_UNSUPPORTED = -3
+BSX_ERR_HIP = -4
+
+DTYPE_BF16 = 0
+DTYPE_FP16 = 1
+DTYPE_FP32 = 2
+
+MASK_NONE = 0
+MASK_CAUSAL = 1
+MASK_TREE = 2
+MASK_STREAMING = 3
+
+
+class AttnPlan(ctypes.Structure):
+    """Mirror of ``bsx_attn_plan_t``."""
+
+    _fields_ = [
+        ("batch", c_int32),
+        ("num_qo_heads", c_int32),
+        ("num_kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("page_size", c_int32),
+        ("mask_mode", c_int32),
+        ("group_size", c_int32),
+        ("qrow_tile", c_int32),
+        ("qrow_blocks", c_int32),
+        ("heads_per_cta", c_int32),
+        ("qblocks_per_cta", c_int32),
+        ("num_qgroups", c_int32),
+        ("num_ctas", c_int32),
+        ("num_segments", c_int32),
+        ("num_partials", c_int32),
+        ("num_merge_seqs", c_int32),
+        ("max_qo_len", c_int32),
+        ("tile_tokens", c_int32),
+        ("sink_tokens", c_int32),
+        ("window_tokens", c_int32),
+        ("off_seq", c_int32),
+        ("off_seg_indptr", c_int32),
+        ("off_segments", c_int32),
+        ("off_merge_seqs", c_int32),
+        ("off_part_indptr", c_int32),
+        ("plan_ints", c_int32),
+        ("float_ws_bytes", c_int64),
+        ("sm_scale", c_float),
+        ("total_qo", c_int32),
+    ]
+
+
+_P = c_void_p  # every tensor pointer crosses the ABI as a plain address
+_PI32 = POINTER(c_int32)
+
+# name -> (restype, argtypes); must match include/bsx.h exactly.
+SIGNATURES = {
+    "bsx_last_error": (ctypes.c_char_p, []),
+    "bsx_version": (c_int, []),
+    "bsx_attn_plan_ints_bound": (c_int64, [c_int, c_int]),
+    "bsx_attn_plan": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                              c_float, c_int, _P, c_int64, POINTER(AttnPlan)]),
+    "bsx_attn_run": (c_int, [POINTER(AttnPlan), _P, _P, c_int, _P, c_int64, _P, _P, c_int64, _P,
+                             _P, _P, c_int64, _P, _P]),
+    "bsx_get_seq_lens": (c_int, [_P, _P, c_int, c_int, _P, _P]),
+    "bsx_get_batch_indices_positions": (c_int, [_P, _P, c_int, c_int, _P, _P, _P]),
+    "bsx_append_paged_kv_cache": (c_int, [_P, _P, c_int64, c_int64, _P, _P, c_int, _P, _P, c_int64,
+                                          _P, _P, c_int, c_int, c_int, c_int, _P]),
+    "bsx_kv_append": (c_int, [_P, _P, c_int64, c_int64, _P, _P, _P, _P, c_int, c_int, _P, _P,
+                              c_int64, c_int, c_int, c_int, c_int, _P]),
+    "bsx_argmax_ws_bytes": (c_int64, [c_int64, c_int64]),
+    "bsx_argmax": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, _P]),
+    "bsx_accept_greedy_ws_bytes": (c_int64, [c_int, c_int, c_int64]),
+    "bsx_accept_greedy": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int64, c_int64, c_int, _P, _P,
+                                  _P, _P, c_int64, _P]),
+    "bsx_chain_ws_bytes": (c_int64, [c_int, c_int, c_int64]),
+    "bsx_chain_speculative_sampling": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int64, _P, _P, _P,
+                                               _P, c_int64, _P]),
+    "bsx_chain_speculative_sampling_logits": (c_int, [_P, _P, _P, c_int, c_float, _P, c_int, c_int,
+                                                      c_int64, _P, _P, _P, _P, c_int64, _P]),
+    "bsx_softmax_ws_bytes": (c_int64, [c_int64]),
+    "bsx_softmax": (c_int, [_P, c_int, c_float, c_int64, c_int64, _P, _P, c_int64, _P]),
+}
+
+_lib = None
+
+
+class BsxError(RuntimeError):
+    """A bsx entry point returned an error status."""
+
+
+def load() -> ctypes.CDLL:
+    """Load libbsx.so once and bind every entry point; raise if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is not built: run `python -m batchspec_amd.build` "
+            "(the HIP library is the only compute path of batchspec_amd)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise the Python exception matching a bsx status code."""
+    if rc == BSX_OK:
+        return
+    msg = load().bsx_last_error().decode(errors="replace")
+    text = f"{what}: {msg}"
+    if rc in (BSX_ERR_INVALID, BSX_ERR_CAPACITY):
+        raise ValueError(text)
+    if rc == BSX_ERR_UNSUPPORTED:
+        raise NotImplementedError(text)
+    raise BsxError(text)
+
+
+def ptr(t) -> int | None:
+    """Device (or host) address of a tensor, None for None."""
+    return None if t is None else t.data_ptr()

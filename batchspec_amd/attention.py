@@ -1,0 +1,324 @@
+"""Verify attention behind FlashInfer's ``BatchPrefillWithPagedKVCacheWrapper`` surface.
+
+BatchSpec builds the wrapper at batchspec/backends/base/attn_wrapper.py:53-72
+(NHD layout, ``use_cuda_graph=True``, fixed page-table buffers, optional custom-mask
+buffers), plans it once per step (batchspec/backends/standard_engine.py:132-143,
+batchspec/backends/mtp_engine.py:331-342,420-432,486-497) and runs it in every layer
+(batchspec/models/modules/attention/standard.py:69).  This class keeps that
+constructor, ``plan`` and ``run``; the compute is the gfx950 kernel of
+``libbsx.so``.
+
+Supported plan options: ``causal`` (bottom-right aligned), ``custom_mask`` whose
+prefix columns are all visible and whose last ``qo_len`` columns form an at most
+32-wide block (the MTP and EAGLE-tree masks), or the equivalent per-query-token
+``tree_mask_words``; and a StreamingLLM sink + window view (``sink_tokens``,
+``window_tokens``) for MagicDec-style draft attention.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence, Tuple, Union
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._util import dtype_code, num_cus, require_gpu, stream_of
+
+_ALIGN = 256
+
+
+def _align(n: int) -> int:
+    return (n + _ALIGN - 1) // _ALIGN * _ALIGN
+
+
+def _host_i32(t: torch.Tensor) -> np.ndarray:
+    return np.ascontiguousarray(t.detach().to("cpu", torch.int32).numpy())
+
+
+def custom_mask_to_tree_words(custom_mask: torch.Tensor, qo_lens: np.ndarray,
+                              kv_lens: np.ndarray) -> np.ndarray:
+    """Flattened per-request bool masks [qo_len x kv_len] -> one uint32 per query token.
+
+    Bit c of the word of query token t is mask[t, kv_len - qo_len + c].  Raises
+    NotImplementedError unless every request attends to all of its first
+    kv_len - qo_len tokens and qo_len <= 32 (the layout of
+    batchspec/backends/mtp_engine.py:410-417).
+    """
+    m = custom_mask.detach().to("cpu", torch.bool).numpy().reshape(-1)
+    need = int(np.sum(qo_lens.astype(np.int64) * kv_lens.astype(np.int64)))
+    if m.size < need:
+        raise ValueError(f"custom_mask has {m.size} entries, the page table needs {need}")
+    words = np.zeros(int(qo_lens.sum()), dtype=np.uint32)
+    off = 0
+    row0 = 0
+    for q, kv in zip(qo_lens.tolist(), kv_lens.tolist()):
+        blk = m[off:off + q * kv].reshape(q, kv) if q > 0 else m[0:0].reshape(0, kv)
+        off += q * kv
+        if q == 0:
+            continue
+        if q > 32 or kv < q:
+            raise NotImplementedError(
+                "custom masks are supported when qo_len <= 32 <= kv_len pattern holds "
+                f"(got qo_len={q}, kv_len={kv})")
+        if not blk[:, :kv - q].all():
+            raise NotImplementedError(
+                "custom masks must attend to every prefix token (kv_len - qo_len columns)")
+        tail = blk[:, kv - q:].astype(np.uint64)
+        words[row0:row0 + q] = (tail << np.arange(q, dtype=np.uint64)).sum(axis=1).astype(np.uint32)
+        row0 += q
+    return words
+
+
+class BatchPrefillWithPagedKVCacheWrapper:
+    """Paged-KV attention for ragged batches of verify / prefill queries (gfx950)."""
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
+                 use_cuda_graph: bool = False, qo_indptr_buf: Optional[torch.Tensor] = None,
+                 paged_kv_indptr_buf: Optional[torch.Tensor] = None,
+                 paged_kv_indices_buf: Optional[torch.Tensor] = None,
+                 paged_kv_last_page_len_buf: Optional[torch.Tensor] = None,
+                 custom_mask_buf: Optional[torch.Tensor] = None,
+                 mask_indptr_buf: Optional[torch.Tensor] = None,
+                 backend: str = "auto", **unused) -> None:
+        if kv_layout != "NHD":
+            raise NotImplementedError(f"kv_layout {kv_layout!r}: only 'NHD' is implemented")
+        if backend not in ("auto", "bsx"):
+            raise NotImplementedError(f"backend {backend!r}")
+        self._device = require_gpu("workspace", float_workspace_buffer)
+        _lib.load()
+        self._ws = float_workspace_buffer.view(torch.uint8).reshape(-1)
+        self._use_cuda_graph = bool(use_cuda_graph)
+        self._qo_indptr_buf = qo_indptr_buf
+        self._kv_indptr_buf = paged_kv_indptr_buf
+        self._kv_indices_buf = paged_kv_indices_buf
+        self._kv_last_buf = paged_kv_last_page_len_buf
+        self._custom_mask_buf = custom_mask_buf
+        self._mask_indptr_buf = mask_indptr_buf
+        if self._use_cuda_graph and paged_kv_indices_buf is None:
+            raise ValueError("use_cuda_graph=True needs paged_kv_indices_buf")
+        self._num_cus = num_cus(self._device.index if self._device.index is not None
+                                else torch.cuda.current_device())
+        self._plan: Optional[_lib.AttnPlan] = None
+        self._kv_indices: Optional[torch.Tensor] = None
+        self._mask_words: Optional[torch.Tensor] = None
+        self._blob_bytes = 0
+        self._pinned: Optional[torch.Tensor] = None
+        self._copy_done: Optional[torch.cuda.Event] = None
+        self._dtype: Optional[torch.dtype] = None
+
+    # ------------------------------------------------------------------ plan
+    def plan(self, qo_indptr: torch.Tensor, paged_kv_indptr: torch.Tensor,
+             paged_kv_indices: torch.Tensor, paged_kv_last_page_len: torch.Tensor,
+             num_qo_heads: int, num_kv_heads: int, head_dim_qk: int, page_size: int,
+             head_dim_vo: Optional[int] = None, custom_mask: Optional[torch.Tensor] = None,
+             packed_custom_mask: Optional[torch.Tensor] = None, causal: bool = False,
+             pos_encoding_mode: str = "NONE", use_fp16_qk_reduction: bool = False,
+             sm_scale: Optional[float] = None, window_left: int = -1,
+             logits_soft_cap: Optional[float] = None, rope_scale: Optional[float] = None,
+             rope_theta: Optional[float] = None, q_data_type: Union[str, torch.dtype] = "float16",
+             kv_data_type: Union[str, torch.dtype, None] = None, non_blocking: bool = True,
+             *, tree_mask_words: Optional[torch.Tensor] = None, sink_tokens: int = 0,
+             window_tokens: int = 0) -> None:
+        """Schedule one step of attention; shared by every layer until the next plan.
+
+        Mirrors FlashInfer's plan (arguments as passed at
+        batchspec/backends/standard_engine.py:132-143).  Host-synchronising: the
+        indptr arrays are read on the host, as FlashInfer does.
+        """
+        if head_dim_vo is not None and head_dim_vo != head_dim_qk:
+            raise NotImplementedError("head_dim_vo != head_dim_qk")
+        if packed_custom_mask is not None:
+            raise NotImplementedError("packed_custom_mask; pass custom_mask or tree_mask_words")
+        if pos_encoding_mode != "NONE":
+            raise NotImplementedError("RoPE is applied by the caller (pos_encoding_mode='NONE')")
+        if logits_soft_cap not in (None, 0.0) or window_left not in (-1, None):
+            raise NotImplementedError("logits_soft_cap / window_left")
+        if use_fp16_qk_reduction:
+            raise NotImplementedError("use_fp16_qk_reduction")
+        qdt = _as_dtype(q_data_type)
+        if qdt not in (torch.bfloat16, torch.float16):
+            raise NotImplementedError(f"q_data_type {qdt}: bf16 and fp16 are implemented")
+        kdt = _as_dtype(kv_data_type) if kv_data_type is not None else qdt
+        if kdt != qdt:
+            raise NotImplementedError("kv_data_type must equal q_data_type")
+
+        qo_h = _host_i32(qo_indptr)
+        kvp_h = _host_i32(paged_kv_indptr)
+        last_h = _host_i32(paged_kv_last_page_len)
+        batch = int(qo_h.shape[0]) - 1
+        if batch < 0 or kvp_h.shape[0] != batch + 1 or last_h.shape[0] < batch:
+            raise ValueError("qo_indptr, paged_kv_indptr and paged_kv_last_page_len disagree on batch")
+        last_h = np.ascontiguousarray(last_h[:batch])
+
+        streaming = sink_tokens > 0 or window_tokens > 0
+        words = None
+        if tree_mask_words is not None or custom_mask is not None:
+            if causal or streaming:
+                raise ValueError("custom/tree mask cannot be combined with causal or streaming")
+            mode = _lib.MASK_TREE
+            if tree_mask_words is not None:
+                words = tree_mask_words
+            else:
+                qo_lens = np.diff(qo_h)
+                npages = np.diff(kvp_h)
+                kv_lens = np.where(npages > 0, (npages - 1) * page_size + last_h, 0)
+                words = custom_mask_to_tree_words(custom_mask, qo_lens, kv_lens)
+        elif streaming:
+            mode = _lib.MASK_STREAMING
+        elif causal:
+            mode = _lib.MASK_CAUSAL
+        else:
+            mode = _lib.MASK_NONE
+
+        lib = _lib.load()
+        bound = int(lib.bsx_attn_plan_ints_bound(batch, self._num_cus))
+        blob = np.empty(bound, dtype=np.int32)
+        plan = _lib.AttnPlan()
+        rc = lib.bsx_attn_plan(qo_h.ctypes.data, kvp_h.ctypes.data, last_h.ctypes.data, batch,
+                               int(num_qo_heads), int(num_kv_heads), int(head_dim_qk),
+                               int(page_size), mode, int(sink_tokens), int(window_tokens),
+                               float(sm_scale) if sm_scale else 0.0, self._num_cus,
+                               blob.ctypes.data, bound, ctypes.byref(plan))
+        _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan")
+
+        if self._use_cuda_graph:
+            # the float region must not move between plans of a captured graph: size the
+            # blob region for the largest batch the registered buffers allow
+            max_batch = batch if self._qo_indptr_buf is None else max(
+                batch, self._qo_indptr_buf.numel() - 1)
+            region = _align(int(lib.bsx_attn_plan_ints_bound(max_batch, self._num_cus)) * 4)
+            blob_bytes = max(self._blob_bytes, region)
+        else:
+            blob_bytes = _align(bound * 4)
+        need = blob_bytes + int(plan.float_ws_bytes)
+        if need > self._ws.numel():
+            raise ValueError(f"float_workspace_buffer too small: need {need} bytes, "
+                             f"have {self._ws.numel()}")
+        self._blob_bytes = blob_bytes
+
+        # Stage the blob through pinned memory; the previous copy must have landed
+        # before its staging buffer is rewritten.
+        n = int(plan.plan_ints)
+        if self._pinned is None or self._pinned.numel() < bound:
+            if self._copy_done is not None:
+                self._copy_done.synchronize()
+            self._pinned = torch.empty(bound, dtype=torch.int32, pin_memory=True)
+        elif self._copy_done is not None:
+            self._copy_done.synchronize()
+        self._pinned[:n].copy_(torch.from_numpy(blob[:n]))
+        dev_blob = self._ws[:n * 4].view(torch.int32)
+        with torch.cuda.device(self._device):
+            dev_blob.copy_(self._pinned[:n], non_blocking=True)
+            if self._copy_done is None:
+                self._copy_done = torch.cuda.Event()
+            self._copy_done.record()
+
+        # Page ids: in graph mode run() reads the registered buffer.
+        if self._use_cuda_graph:
+            nidx = paged_kv_indices.numel()
+            if nidx > self._kv_indices_buf.numel():
+                raise ValueError("paged_kv_indices larger than paged_kv_indices_buf")
+            if paged_kv_indices.data_ptr() != self._kv_indices_buf.data_ptr():
+                self._kv_indices_buf[:nidx].copy_(paged_kv_indices, non_blocking=non_blocking)
+            self._kv_indices = self._kv_indices_buf
+        else:
+            self._kv_indices = paged_kv_indices
+        require_gpu("plan", self._kv_indices)
+        if self._kv_indices.dtype != torch.int32:
+            raise ValueError("paged_kv_indices must be int32")
+
+        if words is not None:
+            if isinstance(words, torch.Tensor):
+                w = words.to(torch.int32)
+            else:
+                w = torch.from_numpy(np.ascontiguousarray(
+                    np.asarray(words, dtype=np.uint32).view(np.int32)))
+            if w.numel() < int(plan.total_qo):
+                raise ValueError("tree_mask_words needs one word per query token")
+            w = w.reshape(-1)[: int(plan.total_qo)]
+            if self._mask_words is None or self._mask_words.numel() < w.numel():
+                if self._use_cuda_graph and self._mask_words is not None:
+                    raise ValueError("mask grew beyond its cuda-graph buffer")
+                cap = max(w.numel(), 1)
+                if self._use_cuda_graph and self._qo_indptr_buf is not None:
+                    cap = max(cap, 32 * (self._qo_indptr_buf.numel()))
+                self._mask_words = torch.zeros(cap, dtype=torch.int32, device=self._device)
+            self._mask_words[: w.numel()].copy_(w, non_blocking=True)
+        self._plan = plan
+        self._dtype = qdt
+
+    # ------------------------------------------------------------------- run
+    def run(self, q: torch.Tensor,
+            paged_kv_cache: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]],
+            out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+            return_lse: bool = False, **unused):
+        """Attention output [nnz, num_qo_heads, head_dim] (and lse [nnz, num_qo_heads])."""
+        plan = self._plan
+        if plan is None:
+            raise RuntimeError("plan() must be called before run()")
+        k_cache, v_cache, page_stride = _split_cache(paged_kv_cache, plan)
+        dev = require_gpu("run", q, k_cache, v_cache)
+        if q.dtype != k_cache.dtype or q.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError(f"q ({q.dtype}) and paged_kv_cache ({k_cache.dtype}) must both be "
+                             "bf16 or fp16")
+        if q.dim() != 3 or tuple(q.shape[1:]) != (plan.num_qo_heads, plan.head_dim) \
+                or q.shape[0] != plan.total_qo:
+            raise ValueError(f"q shape {tuple(q.shape)} does not match the plan "
+                             f"[{plan.total_qo}, {plan.num_qo_heads}, {plan.head_dim}]")
+        if q.stride(2) != 1 or q.stride(1) != plan.head_dim:
+            q = q.contiguous()
+        if out is None:
+            out = torch.empty((plan.total_qo, plan.num_qo_heads, plan.head_dim), dtype=q.dtype,
+                              device=dev)
+        elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 \
+                or out.stride(1) != plan.head_dim:
+            raise ValueError("out must match q in shape and dtype with dense heads")
+        if return_lse and lse is None:
+            lse = torch.empty((plan.total_qo, plan.num_qo_heads), dtype=torch.float32, device=dev)
+        if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()):
+            raise ValueError("lse must be a contiguous float32 tensor")
+        ws = self._ws
+        blob = ws[: int(plan.plan_ints) * 4]
+        fws = ws[self._blob_bytes:] if int(plan.float_ws_bytes) > 0 else None
+        lib = _lib.load()
+        rc = lib.bsx_attn_run(ctypes.byref(plan), blob.data_ptr(),
+                              None if fws is None else fws.data_ptr(),
+                              dtype_code(q.dtype), q.data_ptr(), q.stride(0),
+                              k_cache.data_ptr(), v_cache.data_ptr(), page_stride,
+                              self._kv_indices.data_ptr(),
+                              None if self._mask_words is None or plan.mask_mode != _lib.MASK_TREE
+                              else self._mask_words.data_ptr(),
+                              out.data_ptr(), out.stride(0), _lib.ptr(lse), stream_of(dev))
+        _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.run")
+        return (out, lse) if return_lse else out
+
+    forward = run
+
+    @property
+    def plan_info(self) -> Optional[_lib.AttnPlan]:
+        return self._plan
+
+
+def _as_dtype(d) -> torch.dtype:
+    if isinstance(d, torch.dtype):
+        return d
+    return getattr(torch, str(d).replace("torch.", ""))
+
+
+def _split_cache(cache, plan) -> Tuple[torch.Tensor, torch.Tensor, int]:
+    """(k view, v view, page stride in elements) for the NHD layouts of the reference."""
+    H, D, ps = plan.num_kv_heads, plan.head_dim, plan.page_size
+    if isinstance(cache, (tuple, list)):
+        k, v = cache
+        if k.dim() != 4 or tuple(k.shape[1:]) != (ps, H, D) or k.shape != v.shape:
+            raise ValueError(f"k/v caches must be [P, {ps}, {H}, {D}]")
+        if k.stride()[1:] != (H * D, D, 1) or v.stride() != k.stride():
+            raise ValueError("k/v caches must be dense within a page and share strides")
+        return k, v, k.stride(0)
+    if cache.dim() != 5 or tuple(cache.shape[1:]) != (2, ps, H, D):
+        raise ValueError(f"paged_kv_cache must be [P, 2, {ps}, {H}, {D}] (NHD), "
+                         f"got {tuple(cache.shape)}")
+    if cache.stride()[1:] != (ps * H * D, H * D, D, 1):
+        raise ValueError("paged_kv_cache must be dense within a page")
+    return cache[:, 0], cache[:, 1], cache.stride(0)

@@ -1,0 +1,830 @@
+// Speculative acceptance (piece 3 of the verification path) and softmax.
+//
+// Greedy: MTPEngine.evaluate_posterior greedy branch
+// (batchspec/backends/mtp_engine.py:553-560) with the argmax of
+// mtp_engine.py:747 fused in:
+//   flags_i = preds_i == draft_i;  accept = sum(flags)+1 (reference rule) or the
+//   longest matching prefix + 1;  bonus = preds[accept-1];
+//   eos_accepted = any(draft_i == eos and flags_i).
+// Argmax follows torch.argmax: the first maximum wins and NaN counts as maximum.
+//
+// Stochastic: chain speculative sampling (the FlashInfer call at
+// mtp_engine.py:569) with caller-supplied uniforms u[B, k+1]:
+//   accept draft token x_i  iff  u_i * q_i(x_i) < p_i(x_i),  i = 0..k-1 in order;
+//   at the first rejection j, emit a draw from max(0, p_j - q_j) (normalised) using
+//   u_k; if all k are accepted, emit a draw from p_k using u_k.
+// All floating-point values the decisions depend on follow the canonical order of
+// canon.h, so the token ids match a CPU restatement bit for bit.  The draw is an
+// inverse-CDF walk down the 2048-lane reduction tree: at each node go left iff
+// t < sum(left) (or the right subtree is empty), else t -= sum(left); inside the
+// chosen lane the groups, then the elements, are scanned left to right.
+//
+// This translation unit is compiled with -ffp-contract=off: every multiply-add
+// that the canonical order fuses is an explicit fmaf.
+#include <algorithm>
+
+#include "common.h"
+#include "canon.h"
+
+namespace bsx {
+namespace acc {
+
+using canon::kGroup;
+using canon::kLanes;
+using canon::LaneState;
+
+// ----------------------------------------------------------------------------
+// Row access: group g of a row of V elements, as fp32 (exact conversion).
+// ----------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ int load_group(const void* row, int64_t g, int64_t V, bool vec,
+                                          float x[8]) {
+  const int64_t v0 = g * kGroup;
+  const int n = (int)min((int64_t)kGroup, V - v0);
+  if constexpr (DT == BSX_DTYPE_FP32) {
+    const float* r = static_cast<const float*>(row) + v0;
+    if (vec && n == 8) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(r);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(r + 4);
+      x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+      x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = e < n ? r[e] : 0.f;
+    }
+  } else {
+    const uint16_t* r = static_cast<const uint16_t*>(row) + v0;
+    if (vec && n == 8) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(r);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        x[2 * q] = lo_f32<DT>(w[q]);
+        x[2 * q + 1] = hi_f32<DT>(w[q]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = e < n ? half_bits_to_f32<DT>(r[e]) : 0.f;
+    }
+  }
+  return n;
+}
+
+template <int DT>
+__device__ __forceinline__ float load_one(const void* row, int64_t v) {
+  if constexpr (DT == BSX_DTYPE_FP32) return static_cast<const float*>(row)[v];
+  else return half_bits_to_f32<DT>(static_cast<const uint16_t*>(row)[v]);
+}
+
+// ----------------------------------------------------------------------------
+// Row statistics (M, Z): online lane states, one rescale per lane to the row max,
+// then the canonical binary tree over lanes.  One 256-thread workgroup per row;
+// thread t owns lanes 8t+i (its groups t + 256*c, lane i = c mod 8).
+// ----------------------------------------------------------------------------
+template <int DT>
+__device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* out_m,
+                          float* out_z) {
+  __shared__ float wave_val[4];
+  const int t = threadIdx.x;
+  const int64_t G = ceil_div(V, kGroup);
+  LaneState st[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    st[i].m = -INFINITY;
+    st[i].s = 0.f;
+  }
+  for (int64_t c0 = 0; (int64_t)t + 256 * c0 < G; c0 += 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t g = (int64_t)t + 256 * (c0 + i);
+      if (g < G) {
+        float x[8];
+        const int n = load_group<DT>(row, g, V, vec, x);
+        float gm = x[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e)
+          if (e < n) gm = fmaxf(gm, x[e]);
+        if (n == 8) {
+          canon::lane_update(st[i], x, 8, gm, c);
+        } else {
+          canon::lane_update(st[i], x, n, gm, c);
+        }
+      }
+    }
+  }
+  // row max (order-free)
+  float mx = st[0].m;
+#pragma unroll
+  for (int i = 1; i < 8; ++i) mx = fmaxf(mx, st[i].m);
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  if ((t & 63) == 0) wave_val[t >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wave_val[0], wave_val[1]), fmaxf(wave_val[2], wave_val[3]));
+  __syncthreads();
+  const float rho_m = mx * c;
+  // lanes 8t+i rescaled once, then the tree over i, over t in the wave, over waves
+  float r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = canon::lane_rescaled(st[i], c, rho_m);
+  float s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) s = s + __shfl_xor(s, m);
+  if ((t & 63) == 0) wave_val[t >> 6] = s;
+  __syncthreads();
+  if (t == 0) {
+    *out_m = mx;
+    *out_z = (wave_val[0] + wave_val[1]) + (wave_val[2] + wave_val[3]);
+  }
+  __syncthreads();
+}
+
+// rows [0, n_a) come from tensor a, rows [n_a, n_a + n_b) from tensor b.
+template <int DT>
+__global__ void __launch_bounds__(256) stats_kernel(const void* a, int64_t n_a, const void* b,
+                                                    int64_t V, float c, float2* stats) {
+  const int64_t r = blockIdx.x;
+  const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
+  const char* base = r < n_a ? static_cast<const char*>(a) + r * V * esz
+                             : static_cast<const char*>(b) + (r - n_a) * V * esz;
+  const bool vec = ((V * esz) % 16 == 0) && (((uintptr_t)base) % 16 == 0);
+  float m, z;
+  row_stats<DT>(base, V, vec, c, &m, &z);
+  if (threadIdx.x == 0) stats[r] = make_float2(m, z);
+}
+
+// ----------------------------------------------------------------------------
+// Chain decision (identical in every kernel that needs it).
+// ----------------------------------------------------------------------------
+struct ChainArgs {
+  // logits path
+  const void* t_logits;  // [B, k+1, V]
+  const void* d_logits;  // [B, k, V] or null (one-hot draft)
+  const float2* stats;   // [B*(k+1)] target rows, then [B*k] draft rows
+  float c;
+  // probs path
+  const float* t_probs;  // [B, k+1, V]
+  const float* d_probs;  // [B, k, V] or null
+  // common
+  const int64_t* draft_ids;  // [B, k]
+  const float* uniforms;     // [B, k+1]
+  int B, k;
+  int64_t V;
+  float* lanes;  // [B, 2048]
+  float* gsum;   // [B, G]
+  int32_t* out_ids;
+  int32_t* accepted;
+  int32_t* emitted;
+};
+
+template <int DT, bool LOGITS>
+struct Chain {
+  const ChainArgs& a;
+  __device__ Chain(const ChainArgs& args) : a(args) {}
+
+  __device__ float2 tstat(int b, int i) const { return a.stats[(int64_t)b * (a.k + 1) + i]; }
+  __device__ float2 dstat(int b, int i) const {
+    return a.stats[(int64_t)a.B * (a.k + 1) + (int64_t)b * a.k + i];
+  }
+  __device__ const void* trow(int b, int i) const {
+    const size_t esz = LOGITS ? (DT == BSX_DTYPE_FP32 ? 4 : 2) : 4;
+    const char* base = LOGITS ? static_cast<const char*>(a.t_logits)
+                              : reinterpret_cast<const char*>(a.t_probs);
+    return base + (((int64_t)b * (a.k + 1) + i) * a.V) * esz;
+  }
+  __device__ const void* drow(int b, int i) const {
+    const size_t esz = LOGITS ? (DT == BSX_DTYPE_FP32 ? 4 : 2) : 4;
+    const char* base = LOGITS ? static_cast<const char*>(a.d_logits)
+                              : reinterpret_cast<const char*>(a.d_probs);
+    return base + (((int64_t)b * a.k + i) * a.V) * esz;
+  }
+  __device__ bool has_draft_dist() const {
+    return LOGITS ? a.d_logits != nullptr : a.d_probs != nullptr;
+  }
+
+  // p_i(v), q_i(v) as defined by the canonical order.
+  __device__ float p_at(int b, int i, int64_t v) const {
+    if constexpr (LOGITS) {
+      const float2 s = tstat(b, i);
+      const float x = load_one<DT>(trow(b, i), v);
+      return canon::weight(x, a.c, -(s.x * a.c)) * (1.0f / s.y);
+    } else {
+      return static_cast<const float*>(trow(b, i))[v];
+    }
+  }
+  __device__ float q_at(int b, int i, int64_t v, int64_t draft_tok) const {
+    if (!has_draft_dist()) return v == draft_tok ? 1.0f : 0.0f;
+    if constexpr (LOGITS) {
+      const float2 s = dstat(b, i);
+      const float x = load_one<DT>(drow(b, i), v);
+      return canon::weight(x, a.c, -(s.x * a.c)) * (1.0f / s.y);
+    } else {
+      return static_cast<const float*>(drow(b, i))[v];
+    }
+  }
+
+  // Returns j (first rejected position, k if none) and the independent accept count.
+  __device__ int decide(int b, int* n_accept) const {
+    int j = a.k, cnt = 0;
+    for (int i = 0; i < a.k; ++i) {
+      const int64_t x = a.draft_ids[(int64_t)b * a.k + i];
+      bool acc = false;
+      if (x >= 0 && x < a.V) {
+        const float p = p_at(b, i, x);
+        const float q = q_at(b, i, x, x);
+        const float u = a.uniforms[(int64_t)b * (a.k + 1) + i];
+        acc = u * q < p;
+      }
+      cnt += acc ? 1 : 0;
+      if (!acc && j == a.k) j = i;
+    }
+    *n_accept = cnt;
+    return j;
+  }
+
+  // Residual weights of group g of row j (j == k: target row k alone).
+  // fallback: weights of p_j (used when the residual has no mass).
+  __device__ int residual_group(int b, int j, int64_t g, bool fallback, float r[8]) const {
+    const int64_t V = a.V;
+    const int64_t x = j < a.k ? a.draft_ids[(int64_t)b * a.k + j] : -1;
+    float xt[8], xd[8];
+    const void* tr = trow(b, j);
+    const bool tvec = (((uintptr_t)tr) % 16 == 0) &&
+                      ((V * (LOGITS && DT != BSX_DTYPE_FP32 ? 2 : 4)) % 16 == 0);
+    const int n = LOGITS ? load_group<DT>(tr, g, V, tvec, xt)
+                         : load_group<BSX_DTYPE_FP32>(tr, g, V, tvec, xt);
+    const bool with_q = j < a.k && !fallback;
+    const bool dist = has_draft_dist();
+    if (with_q && dist) {
+      const void* dr = drow(b, j);
+      const bool dvec = (((uintptr_t)dr) % 16 == 0) &&
+                        ((V * (LOGITS && DT != BSX_DTYPE_FP32 ? 2 : 4)) % 16 == 0);
+      if constexpr (LOGITS) load_group<DT>(dr, g, V, dvec, xd);
+      else load_group<BSX_DTYPE_FP32>(dr, g, V, dvec, xd);
+    }
+    float tnmc = 0.f, tinv = 0.f, dnmc = 0.f, dinv = 0.f;
+    if constexpr (LOGITS) {
+      const float2 ts = tstat(b, j);
+      tnmc = -(ts.x * a.c);
+      tinv = 1.0f / ts.y;
+      if (with_q && dist) {
+        const float2 ds = dstat(b, j);
+        dnmc = -(ds.x * a.c);
+        dinv = 1.0f / ds.y;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float p = 0.f, q = 0.f;
+      if (e < n) {
+        if constexpr (LOGITS) p = canon::weight(xt[e], a.c, tnmc) * tinv;
+        else p = xt[e];
+        if (with_q) {
+          if (dist) {
+            if constexpr (LOGITS) q = canon::weight(xd[e], a.c, dnmc) * dinv;
+            else q = xd[e];
+          } else {
+            q = (g * kGroup + e == x) ? 1.0f : 0.0f;
+          }
+        }
+      }
+      r[e] = with_q ? fmaxf(p - q, 0.0f) : p;
+    }
+    return n;
+  }
+
+  // Lane lam = 8*tt + ii of row j: group sums (stored) and lane sum.
+  __device__ float lane_sum(int b, int j, int lam, bool fallback) const {
+    const int64_t G = ceil_div(a.V, kGroup);
+    const int tt = lam >> 3, ii = lam & 7;
+    float s = 0.f;
+    for (int64_t g = (int64_t)tt + 256 * ii; g < G; g += kLanes) {
+      float r[8];
+      const int n = residual_group(b, j, g, fallback, r);
+      float gs = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (e < n) gs = gs + r[e];
+      a.gsum[(int64_t)b * G + g] = gs;
+      s = s + gs;
+    }
+    return s;
+  }
+};
+
+// grid (B, 8): part w computes the lanes 8*tau + w, tau = threadIdx.x.
+template <int DT, bool LOGITS>
+__global__ void __launch_bounds__(256) residual_kernel(ChainArgs a) {
+  Chain<DT, LOGITS> ch(a);
+  const int b = blockIdx.x;
+  const int w = blockIdx.y;
+  int nacc;
+  const int j = ch.decide(b, &nacc);
+  const int lam = 8 * threadIdx.x + w;
+  a.lanes[(int64_t)b * kLanes + lam] = ch.lane_sum(b, j, lam, false);
+}
+
+// grid B: tree over the 2048 lane sums, inverse-CDF walk, outputs.
+template <int DT, bool LOGITS>
+__global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
+  __shared__ float tree[2 * kLanes];  // level 0 at [0, 2048), level l at [base_l, ...)
+  __shared__ int s_choice;
+  Chain<DT, LOGITS> ch(a);
+  const int b = blockIdx.x;
+  const int t = threadIdx.x;
+  int nacc;
+  const int j = ch.decide(b, &nacc);
+  const int64_t G = ceil_div(a.V, kGroup);
+
+  for (int l = t; l < kLanes; l += 256) tree[l] = a.lanes[(int64_t)b * kLanes + l];
+  __syncthreads();
+  // build levels: level l has 2048>>l nodes at offset off_l = 4096 - (4096 >> l)
+  auto build = [&]() {
+    int off_prev = 0, n_prev = kLanes;
+    while (n_prev > 1) {
+      const int off = off_prev + n_prev;
+      const int n = n_prev >> 1;
+      for (int i = t; i < n; i += 256) tree[off + i] = tree[off_prev + 2 * i] + tree[off_prev + 2 * i + 1];
+      __syncthreads();
+      off_prev = off;
+      n_prev = n;
+    }
+  };
+  build();
+  bool fallback = false;
+  if (!(tree[2 * kLanes - 2] > 0.f)) {
+    // No residual mass (p_j <= q_j everywhere in fp32): draw from p_j instead.
+    fallback = true;
+    __syncthreads();
+    for (int w = 0; w < 8; ++w) tree[8 * t + w] = ch.lane_sum(b, j, 8 * t + w, true);
+    __syncthreads();
+    build();
+  }
+  if (t == 0) {
+    const float u = a.uniforms[(int64_t)b * (a.k + 1) + a.k];
+    const float total = tree[2 * kLanes - 2];
+    float tg = u * total;
+    // descend: node i at level l (offset off_l); children at level l-1: 2i, 2i+1
+    int idx = 0;
+    int offs[12];
+    {
+      int off = 0, n = kLanes, l = 0;
+      while (true) {
+        offs[l] = off;
+        if (n == 1) break;
+        off += n;
+        n >>= 1;
+        ++l;
+      }
+    }
+    for (int l = 11; l >= 1; --l) {
+      const float left = tree[offs[l - 1] + 2 * idx];
+      const float right = tree[offs[l - 1] + 2 * idx + 1];
+      if (tg < left || !(right > 0.f)) {
+        idx = 2 * idx;
+      } else {
+        tg = tg - left;
+        idx = 2 * idx + 1;
+      }
+    }
+    // lane idx: groups in order, then elements
+    const int tt = idx >> 3, ii = idx & 7;
+    const float* gs = a.gsum + (int64_t)b * G;
+    float cacc = 0.f, c_at = 0.f;
+    int64_t chosen = -1, last_pos = -1;
+    float c_last = 0.f;
+    for (int64_t g = (int64_t)tt + 256 * ii; g < G; g += kLanes) {
+      const float gsv = gs[g];
+      const float cn = cacc + gsv;
+      if (gsv > 0.f) {
+        last_pos = g;
+        c_last = cacc;
+      }
+      if (tg < cn) {
+        chosen = g;
+        c_at = cacc;
+        break;
+      }
+      cacc = cn;
+    }
+    if (chosen < 0) {
+      chosen = last_pos;
+      c_at = c_last;
+    }
+    int64_t tok = -1;
+    if (chosen >= 0) {
+      const float tl = tg - c_at;
+      float r[8];
+      const int n = ch.residual_group(b, j, chosen, fallback, r);
+      float s = 0.f;
+      int64_t last_e = -1;
+      for (int e = 0; e < n; ++e) {
+        s = s + r[e];
+        if (r[e] > 0.f) last_e = e;
+        if (tl < s) {
+          tok = chosen * kGroup + e;
+          break;
+        }
+      }
+      if (tok < 0 && last_e >= 0) tok = chosen * kGroup + last_e;
+    }
+    s_choice = (int)tok;
+    int32_t* out = a.out_ids + (int64_t)b * (a.k + 1);
+    for (int i = 0; i <= a.k; ++i) {
+      int32_t v = -1;
+      if (i < j) v = (int32_t)a.draft_ids[(int64_t)b * a.k + i];
+      else if (i == j) v = (int32_t)tok;
+      out[i] = v;
+    }
+    a.accepted[b] = nacc;
+    a.emitted[b] = j;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Softmax: probs = weight(x) / Z with the canonical (M, Z).
+// ----------------------------------------------------------------------------
+template <int DT>
+__global__ void __launch_bounds__(256) softmax_norm_kernel(const void* logits, int64_t V, float c,
+                                                           const float2* stats, float* probs) {
+  const int64_t r = blockIdx.x;
+  const float2 s = stats[r];
+  const float nmc = -(s.x * c);
+  const float inv = 1.0f / s.y;
+  const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
+  const char* row = static_cast<const char*>(logits) + r * V * esz;
+  float* out = probs + r * V;
+  for (int64_t v = (int64_t)blockIdx.y * 256 + threadIdx.x; v < V; v += (int64_t)gridDim.y * 256)
+    out[v] = canon::weight(load_one<DT>(row, v), c, nmc) * inv;
+}
+
+// ----------------------------------------------------------------------------
+// Argmax (torch semantics) in parts; partial results as (value, index).
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ bool better(float av, int64_t ai, float bv, int64_t bi) {
+  const bool an = av != av, bn = bv != bv;
+  if (an || bn) return an && (!bn || ai < bi);
+  return av > bv || (av == bv && ai < bi);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256) argmax_part_kernel(const void* logits, int64_t V,
+                                                          int64_t row_stride, int64_t chunk,
+                                                          float* part_val, int64_t* part_idx) {
+  __shared__ float sv[256];
+  __shared__ int64_t si[256];
+  const int64_t r = blockIdx.x;
+  const int part = blockIdx.y;
+  const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
+  const char* row = static_cast<const char*>(logits) + r * row_stride * esz;
+  const int64_t v0 = (int64_t)part * chunk;
+  const int64_t v1 = min(V, v0 + chunk);
+  float bv = -INFINITY;
+  int64_t bi = INT64_MAX;
+  const bool vec = ((((uintptr_t)row) + v0 * esz) % 16 == 0) && (DT != BSX_DTYPE_FP32);
+  if (vec) {
+    // 8 elements per thread per step, visited in increasing index order per thread
+    for (int64_t v = v0 + 8 * threadIdx.x; v < v1; v += 8 * 256) {
+      if (v + 8 <= v1) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(row + v * esz);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float x0 = lo_f32<DT>(w[q]), x1 = hi_f32<DT>(w[q]);
+          if (better(x0, v + 2 * q, bv, bi)) { bv = x0; bi = v + 2 * q; }
+          if (better(x1, v + 2 * q + 1, bv, bi)) { bv = x1; bi = v + 2 * q + 1; }
+        }
+      } else {
+        for (int64_t u = v; u < v1; ++u) {
+          const float x = load_one<DT>(row, u);
+          if (better(x, u, bv, bi)) { bv = x; bi = u; }
+        }
+      }
+    }
+  } else {
+    for (int64_t v = v0 + threadIdx.x; v < v1; v += 256) {
+      const float x = load_one<DT>(row, v);
+      if (better(x, v, bv, bi)) { bv = x; bi = v; }
+    }
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      const float ov = sv[threadIdx.x + s];
+      const int64_t oi = si[threadIdx.x + s];
+      if (better(ov, oi, sv[threadIdx.x], si[threadIdx.x])) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    part_val[r * gridDim.y + part] = sv[0];
+    part_idx[r * gridDim.y + part] = si[0];
+  }
+}
+
+__device__ __forceinline__ int64_t finish_argmax(const float* pv, const int64_t* pi, int64_t r,
+                                                 int parts) {
+  float bv = pv[r * parts];
+  int64_t bi = pi[r * parts];
+  for (int q = 1; q < parts; ++q) {
+    if (better(pv[r * parts + q], pi[r * parts + q], bv, bi)) {
+      bv = pv[r * parts + q];
+      bi = pi[r * parts + q];
+    }
+  }
+  return bi;
+}
+
+__global__ void argmax_final_kernel(const float* pv, const int64_t* pi, int64_t rows, int parts,
+                                    int64_t* out) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r < rows) out[r] = finish_argmax(pv, pi, r, parts);
+}
+
+__global__ void greedy_eval_kernel(const int64_t* draft, const int64_t* target_ids,
+                                   const float* pv, const int64_t* pi, int parts, int B, int k,
+                                   int64_t eos, int mode, int64_t* bonus, int64_t* accept,
+                                   uint8_t* eos_acc) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  int64_t pred[64 + 1];
+  for (int i = 0; i <= k; ++i) {
+    const int64_t r = (int64_t)b * (k + 1) + i;
+    pred[i] = target_ids ? target_ids[r] : finish_argmax(pv, pi, r, parts);
+  }
+  int64_t n = 0;
+  bool prefix = true;
+  bool eos_hit = false;
+  for (int i = 0; i < k; ++i) {
+    const int64_t d = draft[(int64_t)b * k + i];
+    const bool f = pred[i] == d;
+    if (mode == 0) {
+      n += f ? 1 : 0;
+    } else {
+      prefix = prefix && f;
+      n += prefix ? 1 : 0;
+    }
+    const bool counted = mode == 0 ? f : (prefix && f);
+    eos_hit = eos_hit || (counted && d == eos);
+  }
+  accept[b] = n + 1;
+  bonus[b] = pred[n];
+  eos_acc[b] = eos_hit ? 1 : 0;
+}
+
+static int argmax_parts(int64_t rows, int64_t V) {
+  int64_t p = ceil_div(2048, std::max<int64_t>(rows, 1));
+  p = std::min<int64_t>(p, ceil_div(V, 2048));
+  return (int)std::max<int64_t>(1, std::min<int64_t>(p, 64));
+}
+
+template <int DT>
+static int launch_argmax_parts(const void* logits, int64_t rows, int64_t V, int64_t stride,
+                               int parts, float* pv, int64_t* pi, hipStream_t st) {
+  const int64_t chunk = ceil_div(ceil_div(V, parts), 8) * 8;
+  hipLaunchKernelGGL((argmax_part_kernel<DT>), dim3((unsigned)rows, parts), dim3(256), 0, st,
+                     logits, V, stride, chunk, pv, pi);
+  BSX_LAUNCH_CHECK();
+  return BSX_OK;
+}
+
+static int dispatch_argmax_parts(const void* logits, int dtype, int64_t rows, int64_t V,
+                                 int64_t stride, int parts, float* pv, int64_t* pi,
+                                 hipStream_t st) {
+  switch (dtype) {
+    case BSX_DTYPE_BF16:
+      return launch_argmax_parts<BSX_DTYPE_BF16>(logits, rows, V, stride, parts, pv, pi, st);
+    case BSX_DTYPE_FP16:
+      return launch_argmax_parts<BSX_DTYPE_FP16>(logits, rows, V, stride, parts, pv, pi, st);
+    case BSX_DTYPE_FP32:
+      return launch_argmax_parts<BSX_DTYPE_FP32>(logits, rows, V, stride, parts, pv, pi, st);
+  }
+  set_error("unknown dtype %d", dtype);
+  return BSX_ERR_INVALID;
+}
+
+static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+}  // namespace acc
+}  // namespace bsx
+
+using namespace bsx;
+
+extern "C" int64_t bsx_argmax_ws_bytes(int64_t rows, int64_t vocab) {
+  const int parts = acc::argmax_parts(rows, vocab);
+  return acc::align256(rows * parts * 4) + rows * parts * 8;
+}
+
+extern "C" int bsx_argmax(const void* logits_d, int dtype, int64_t rows, int64_t vocab,
+                          int64_t row_stride, int64_t* out_d, void* ws_d, int64_t ws_bytes,
+                          void* stream) {
+  BSX_REQUIRE(rows >= 0 && vocab > 0, BSX_ERR_INVALID, "bad shape rows=%lld vocab=%lld",
+              (long long)rows, (long long)vocab);
+  if (rows == 0) return BSX_OK;
+  BSX_REQUIRE(logits_d && out_d && ws_d, BSX_ERR_INVALID, "null pointer");
+  BSX_REQUIRE(ws_bytes >= bsx_argmax_ws_bytes(rows, vocab), BSX_ERR_CAPACITY,
+              "argmax workspace too small");
+  const int parts = acc::argmax_parts(rows, vocab);
+  float* pv = static_cast<float*>(ws_d);
+  int64_t* pi = reinterpret_cast<int64_t*>(static_cast<char*>(ws_d) + acc::align256(rows * parts * 4));
+  hipStream_t st = as_stream(stream);
+  int rc = acc::dispatch_argmax_parts(logits_d, dtype, rows, vocab, row_stride, parts, pv, pi, st);
+  if (rc != BSX_OK) return rc;
+  hipLaunchKernelGGL(acc::argmax_final_kernel, dim3((unsigned)ceil_div(rows, 256)), dim3(256), 0,
+                     st, pv, pi, rows, parts, out_d);
+  BSX_LAUNCH_CHECK();
+  return BSX_OK;
+}
+
+extern "C" int64_t bsx_accept_greedy_ws_bytes(int B, int k, int64_t vocab) {
+  return bsx_argmax_ws_bytes((int64_t)B * (k + 1), vocab);
+}
+
+extern "C" int bsx_accept_greedy(const int64_t* draft_d, const int64_t* target_ids_d,
+                                 const void* target_logits_d, int dtype, int B, int k,
+                                 int64_t vocab, int64_t eos_id, int mode, int64_t* bonus_d,
+                                 int64_t* accept_d, uint8_t* eos_acc_d, void* ws_d,
+                                 int64_t ws_bytes, void* stream) {
+  BSX_REQUIRE(B >= 0 && k >= 0 && k <= 64, BSX_ERR_INVALID, "bad B=%d / k=%d (k <= 64)", B, k);
+  BSX_REQUIRE(mode == 0 || mode == 1, BSX_ERR_INVALID, "mode must be 0 or 1");
+  if (B == 0) return BSX_OK;
+  BSX_REQUIRE(bonus_d && accept_d && eos_acc_d && (k == 0 || draft_d), BSX_ERR_INVALID,
+              "null pointer");
+  BSX_REQUIRE(target_ids_d || target_logits_d, BSX_ERR_INVALID, "need target ids or logits");
+  hipStream_t st = as_stream(stream);
+  const int64_t rows = (int64_t)B * (k + 1);
+  float* pv = nullptr;
+  int64_t* pi = nullptr;
+  int parts = 1;
+  if (!target_ids_d) {
+    BSX_REQUIRE(vocab > 0, BSX_ERR_INVALID, "vocab must be > 0");
+    BSX_REQUIRE(ws_d && ws_bytes >= bsx_accept_greedy_ws_bytes(B, k, vocab), BSX_ERR_CAPACITY,
+                "greedy workspace too small");
+    parts = acc::argmax_parts(rows, vocab);
+    pv = static_cast<float*>(ws_d);
+    pi = reinterpret_cast<int64_t*>(static_cast<char*>(ws_d) + acc::align256(rows * parts * 4));
+    int rc = acc::dispatch_argmax_parts(target_logits_d, dtype, rows, vocab, vocab, parts, pv, pi, st);
+    if (rc != BSX_OK) return rc;
+  }
+  hipLaunchKernelGGL(acc::greedy_eval_kernel, dim3((unsigned)ceil_div(B, 64)), dim3(64), 0, st,
+                     draft_d, target_ids_d, pv, pi, parts, B, k, eos_id, mode, bonus_d, accept_d,
+                     eos_acc_d);
+  BSX_LAUNCH_CHECK();
+  return BSX_OK;
+}
+
+static int64_t chain_ws_layout(int B, int k, int64_t V, bool logits, int64_t* off_lanes,
+                               int64_t* off_gsum) {
+  const int64_t rows = (int64_t)B * (2 * k + 1);
+  const int64_t stats = logits ? acc::align256(rows * 8) : 0;
+  *off_lanes = stats;
+  *off_gsum = stats + acc::align256((int64_t)B * canon::kLanes * 4);
+  return *off_gsum + acc::align256((int64_t)B * ceil_div(V, canon::kGroup) * 4);
+}
+
+extern "C" int64_t bsx_chain_ws_bytes(int B, int k, int64_t vocab) {
+  int64_t a, b;
+  return chain_ws_layout(B, k, vocab, true, &a, &b);
+}
+
+template <int DT, bool LOGITS>
+static int launch_chain(acc::ChainArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((acc::residual_kernel<DT, LOGITS>), dim3(a.B, 8), dim3(256), 0, st, a);
+  BSX_LAUNCH_CHECK();
+  hipLaunchKernelGGL((acc::pick_kernel<DT, LOGITS>), dim3(a.B), dim3(256), 0, st, a);
+  BSX_LAUNCH_CHECK();
+  return BSX_OK;
+}
+
+static int check_chain_common(const int64_t* draft_ids_d, const float* uniforms_d, int B, int k,
+                              int64_t vocab, int32_t* out_ids_d, int32_t* accepted_d,
+                              int32_t* emitted_d) {
+  BSX_REQUIRE(B >= 0 && k >= 0 && vocab > 0, BSX_ERR_INVALID, "bad B=%d k=%d vocab=%lld", B, k,
+              (long long)vocab);
+  BSX_REQUIRE(vocab < (1LL << 31), BSX_ERR_UNSUPPORTED, "vocab too large");
+  if (B == 0) return BSX_OK;
+  BSX_REQUIRE(uniforms_d && out_ids_d && accepted_d && emitted_d && (k == 0 || draft_ids_d),
+              BSX_ERR_INVALID, "null pointer");
+  return BSX_OK;
+}
+
+extern "C" int bsx_chain_speculative_sampling(const float* draft_probs_d,
+                                              const int64_t* draft_ids_d,
+                                              const float* target_probs_d,
+                                              const float* uniforms_d, int B, int k,
+                                              int64_t vocab, int32_t* out_ids_d,
+                                              int32_t* accepted_d, int32_t* emitted_d, void* ws_d,
+                                              int64_t ws_bytes, void* stream) {
+  int rc = check_chain_common(draft_ids_d, uniforms_d, B, k, vocab, out_ids_d, accepted_d, emitted_d);
+  if (rc != BSX_OK || B == 0) return rc;
+  BSX_REQUIRE(target_probs_d, BSX_ERR_INVALID, "null target_probs");
+  int64_t off_lanes, off_gsum;
+  const int64_t need = chain_ws_layout(B, k, vocab, false, &off_lanes, &off_gsum);
+  BSX_REQUIRE(ws_d && ws_bytes >= need, BSX_ERR_CAPACITY, "chain workspace too small (%lld < %lld)",
+              (long long)ws_bytes, (long long)need);
+  acc::ChainArgs a{};
+  a.t_probs = target_probs_d;
+  a.d_probs = draft_probs_d;
+  a.draft_ids = draft_ids_d;
+  a.uniforms = uniforms_d;
+  a.B = B;
+  a.k = k;
+  a.V = vocab;
+  a.lanes = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_lanes);
+  a.gsum = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_gsum);
+  a.out_ids = out_ids_d;
+  a.accepted = accepted_d;
+  a.emitted = emitted_d;
+  return launch_chain<BSX_DTYPE_FP32, false>(a, as_stream(stream));
+}
+
+template <int DT>
+static int chain_logits_impl(acc::ChainArgs& a, hipStream_t st) {
+  const int64_t n_t = (int64_t)a.B * (a.k + 1);
+  const int64_t n_d = a.d_logits ? (int64_t)a.B * a.k : 0;
+  float2* stats = const_cast<float2*>(a.stats);
+  hipLaunchKernelGGL((acc::stats_kernel<DT>), dim3((unsigned)(n_t + n_d)), dim3(256), 0, st,
+                     a.t_logits, n_t, a.d_logits, a.V, a.c, stats);
+  BSX_LAUNCH_CHECK();
+  return launch_chain<DT, true>(a, st);
+}
+
+extern "C" int bsx_chain_speculative_sampling_logits(const void* draft_logits_d,
+                                                     const int64_t* draft_ids_d,
+                                                     const void* target_logits_d, int dtype,
+                                                     float temperature, const float* uniforms_d,
+                                                     int B, int k, int64_t vocab,
+                                                     int32_t* out_ids_d, int32_t* accepted_d,
+                                                     int32_t* emitted_d, void* ws_d,
+                                                     int64_t ws_bytes, void* stream) {
+  int rc = check_chain_common(draft_ids_d, uniforms_d, B, k, vocab, out_ids_d, accepted_d, emitted_d);
+  if (rc != BSX_OK || B == 0) return rc;
+  BSX_REQUIRE(target_logits_d, BSX_ERR_INVALID, "null target_logits");
+  BSX_REQUIRE(temperature > 0.f && temperature == temperature, BSX_ERR_INVALID,
+              "temperature must be > 0 (greedy acceptance has its own entry point)");
+  int64_t off_lanes, off_gsum;
+  const int64_t need = chain_ws_layout(B, k, vocab, true, &off_lanes, &off_gsum);
+  BSX_REQUIRE(ws_d && ws_bytes >= need, BSX_ERR_CAPACITY, "chain workspace too small (%lld < %lld)",
+              (long long)ws_bytes, (long long)need);
+  acc::ChainArgs a{};
+  a.t_logits = target_logits_d;
+  a.d_logits = draft_logits_d;
+  a.stats = static_cast<const float2*>(ws_d);
+  a.c = canon::scale_for_temperature(temperature);
+  a.draft_ids = draft_ids_d;
+  a.uniforms = uniforms_d;
+  a.B = B;
+  a.k = k;
+  a.V = vocab;
+  a.lanes = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_lanes);
+  a.gsum = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_gsum);
+  a.out_ids = out_ids_d;
+  a.accepted = accepted_d;
+  a.emitted = emitted_d;
+  hipStream_t st = as_stream(stream);
+  switch (dtype) {
+    case BSX_DTYPE_BF16: return chain_logits_impl<BSX_DTYPE_BF16>(a, st);
+    case BSX_DTYPE_FP16: return chain_logits_impl<BSX_DTYPE_FP16>(a, st);
+    case BSX_DTYPE_FP32: return chain_logits_impl<BSX_DTYPE_FP32>(a, st);
+  }
+  set_error("unknown dtype %d", dtype);
+  return BSX_ERR_INVALID;
+}
+
+extern "C" int64_t bsx_softmax_ws_bytes(int64_t rows) { return acc::align256(rows * 8); }
+
+template <int DT>
+static int softmax_impl(const void* logits, int64_t rows, int64_t V, float c, float* probs,
+                        float2* stats, hipStream_t st) {
+  hipLaunchKernelGGL((acc::stats_kernel<DT>), dim3((unsigned)rows), dim3(256), 0, st, logits,
+                     rows, nullptr, V, c, stats);
+  BSX_LAUNCH_CHECK();
+  const int parts = (int)std::min<int64_t>(64, std::max<int64_t>(1, ceil_div(V, 4096)));
+  hipLaunchKernelGGL((acc::softmax_norm_kernel<DT>), dim3((unsigned)rows, parts), dim3(256), 0, st,
+                     logits, V, c, stats, probs);
+  BSX_LAUNCH_CHECK();
+  return BSX_OK;
+}
+
+extern "C" int bsx_softmax(const void* logits_d, int dtype, float temperature, int64_t rows,
+                           int64_t vocab, float* probs_d, void* ws_d, int64_t ws_bytes,
+                           void* stream) {
+  BSX_REQUIRE(rows >= 0 && vocab > 0, BSX_ERR_INVALID, "bad shape");
+  if (rows == 0) return BSX_OK;
+  BSX_REQUIRE(logits_d && probs_d && ws_d, BSX_ERR_INVALID, "null pointer");
+  BSX_REQUIRE(temperature > 0.f, BSX_ERR_INVALID, "temperature must be > 0");
+  BSX_REQUIRE(ws_bytes >= bsx_softmax_ws_bytes(rows), BSX_ERR_CAPACITY, "softmax workspace too small");
+  const float c = canon::scale_for_temperature(temperature);
+  float2* stats = static_cast<float2*>(ws_d);
+  hipStream_t st = as_stream(stream);
+  switch (dtype) {
+    case BSX_DTYPE_BF16: return softmax_impl<BSX_DTYPE_BF16>(logits_d, rows, vocab, c, probs_d, stats, st);
+    case BSX_DTYPE_FP16: return softmax_impl<BSX_DTYPE_FP16>(logits_d, rows, vocab, c, probs_d, stats, st);
+    case BSX_DTYPE_FP32: return softmax_impl<BSX_DTYPE_FP32>(logits_d, rows, vocab, c, probs_d, stats, st);
+  }
+  set_error("unknown dtype %d", dtype);
+  return BSX_ERR_INVALID;
+}

@@ -1,0 +1,103 @@
+// Deterministic ("canonical") arithmetic of the acceptance and softmax kernels.
+//
+// Acceptance must give bit-identical token ids on the GPU and on a CPU restatement
+// fed the same uniforms.  That requires every floating-point value the decisions
+// depend on to be produced by the same sequence of IEEE-754 binary32 operations:
+//   * exp is our own: 2^y = 2^n * P(f), n = rint(y), f = y - n in [-1/2, 1/2], P the
+//     degree-6 Taylor polynomial of 2^f (coefficients ln2^k/k! rounded to binary32),
+//     evaluated by Horner with fused multiply-add; max relative error 1.6e-7.
+//     Arguments below -200 are clamped (2^-200 underflows to 0 in ldexp).
+//   * every sum runs over a fixed tree, independent of the launch configuration:
+//       - a row of V values is cut into groups of 8 consecutive elements
+//         (group g = elements [8g, 8g+8) ∩ [0, V));
+//       - the groups are dealt to NL = 2048 lanes: lane λ = 8t + i owns groups
+//         g = t + 256*i + 2048*j for j = 0, 1, ... (t < 256, i < 8);
+//       - a group sum adds its elements left to right starting from 0;
+//       - a lane sum adds its group sums in increasing j starting from 0;
+//       - the row sum is the balanced binary tree over the 2048 lane sums
+//         (node = left child + right child).
+//   * softmax statistics use the same lanes with an online maximum.  A lane keeps
+//     its running max m and the reference rho(m) = fl(m·C), C = log2(e) * (1/T);
+//     its elements are weighted 2^fma(x, C, -rho(m)).  When a group max gm exceeds
+//     m: s *= 2^(rho(m) - rho(gm)) and m = gm; then s += the group sum of weights.
+//     The row max M is the max over lanes; the row sum Z is the binary tree over
+//     lanes of s_lane·2^(rho(m_lane) - rho(M)) (each lane rescaled exactly once).
+//     Later weights are 2^fma(x, C, -rho(M)).
+// Inputs are finite (a row needs at least one finite logit).
+#pragma once
+
+#include <math.h>
+#include <stdint.h>
+
+#ifndef __HIP__
+#define BSX_HD inline
+#else
+#define BSX_HD __host__ __device__ inline __attribute__((always_inline))
+#endif
+
+namespace bsx {
+namespace canon {
+
+constexpr int kGroup = 8;         // elements per group
+constexpr int kThreads = 256;     // t range
+constexpr int kLanesPerThread = 8;  // i range
+constexpr int kLanes = kThreads * kLanesPerThread;  // 2048
+constexpr int kLaneStride = kLanes;                  // groups between consecutive j
+
+constexpr float kLog2e = 0x1.715476p+0f;
+constexpr float kC0 = 0x1.0p+0f;
+constexpr float kC1 = 0x1.62e430p-1f;
+constexpr float kC2 = 0x1.ebfbe0p-3f;
+constexpr float kC3 = 0x1.c6b08ep-5f;
+constexpr float kC4 = 0x1.3b2ab6p-7f;
+constexpr float kC5 = 0x1.5d87fep-10f;
+constexpr float kC6 = 0x1.430912p-13f;
+
+BSX_HD float exp2(float y) {
+  y = fmaxf(y, -200.0f);
+  float n = rintf(y);
+  float f = y - n;
+  float p = kC6;
+  p = fmaf(p, f, kC5);
+  p = fmaf(p, f, kC4);
+  p = fmaf(p, f, kC3);
+  p = fmaf(p, f, kC2);
+  p = fmaf(p, f, kC1);
+  p = fmaf(p, f, kC0);
+  return ldexpf(p, (int)n);
+}
+
+// Scale C = log2(e) / T.
+BSX_HD float scale_for_temperature(float temperature) {
+  float inv_t = 1.0f / temperature;
+  return kLog2e * inv_t;
+}
+
+// Weight of a logit relative to the row max: 2^(fma(x, C, -(M*C))).
+BSX_HD float weight(float x, float c, float neg_mc) { return exp2(fmaf(x, c, neg_mc)); }
+
+// Online lane state: running max m (reference rho = m*C) and weight sum s.
+struct LaneState {
+  float m;
+  float s;
+};
+
+// Fold one group (n elements, group max gm) into a lane.
+BSX_HD void lane_update(LaneState& st, const float* x, int n, float gm, float c) {
+  if (gm > st.m) {
+    st.s = st.s * exp2(st.m * c - gm * c);
+    st.m = gm;
+  }
+  const float neg_rho = -(st.m * c);
+  float gs = 0.f;
+  for (int e = 0; e < n; ++e) gs = gs + weight(x[e], c, neg_rho);
+  st.s = st.s + gs;
+}
+
+// A lane's sum expressed relative to the row max M (rho_m = M*C).
+BSX_HD float lane_rescaled(LaneState st, float c, float rho_m) {
+  return st.s * exp2(st.m * c - rho_m);
+}
+
+}  // namespace canon
+}  // namespace bsx

@@ -1,0 +1,261 @@
+// Host-side planner of the verify-attention kernel (pure C++, no GPU needed).
+//
+// Plays the role of BatchPrefillWithPagedKVCacheWrapper.plan() as called at
+// batchspec/backends/standard_engine.py:132-143 and
+// batchspec/backends/mtp_engine.py:420-432: it reads the host copies of the CSR
+// page table, validates them, derives every request's kv length with the
+// get_seq_lens formula (batchspec/models/modules/kv_cache.py:66-70), and cuts the
+// whole kv work into equal shares for a persistent grid.
+//
+// Device blob layout (int32):
+//   seq[batch][4]      qo_start, qo_len, kv_len, page_start
+//   seg_indptr[ctas+1] segments of workgroup w are [seg_indptr[w], seg_indptr[w+1])
+//   segments[S][4]     request, first tile, end tile, partial slot (-1 = final)
+//   merge_seqs[M]      requests whose kv range spans several segments
+//   part_indptr[b+1]   partial slots of request b are [part_indptr[b], part_indptr[b+1])
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "../../include/bsx.h"
+
+namespace bsx {
+void set_error(const char* fmt, ...);
+}
+
+#define PLAN_REQUIRE(cond, code, ...)  \
+  do {                                 \
+    if (!(cond)) {                     \
+      ::bsx::set_error(__VA_ARGS__);   \
+      return (code);                   \
+    }                                  \
+  } while (0)
+
+namespace {
+
+constexpr int kTileTokens = 32;
+constexpr int kMaxWavesPerCta = 8;
+
+struct Unit {
+  int b;
+  int tb;
+  int te;
+};
+
+}  // namespace
+
+// Resident waves per SIMD of each kernel variant (from the compiler's register
+// report: D=128 uses 164/224 VGPRs for 16/32 query rows, D=64 108/148).
+static int waves_per_simd(int head_dim, int qrow_tile) {
+  if (head_dim == 128) return qrow_tile == 16 ? 3 : 2;
+  return qrow_tile == 16 ? 4 : 3;
+}
+
+extern "C" int64_t bsx_attn_plan_ints_bound(int batch, int num_cus) {
+  if (batch < 0 || num_cus < 1) return -1;
+  const int64_t num_ctas = (int64_t)num_cus * 16;
+  // seq 4B + seg_indptr (W+1) + segments 4*(W + 2B) + merge B + part_indptr (B+1)
+  return 4LL * batch + (num_ctas + 1) + 4LL * (num_ctas + 2LL * batch) + batch + (batch + 1) + 16;
+}
+
+extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                             const int32_t* kv_last_page_len_h, int batch, int num_qo_heads,
+                             int num_kv_heads, int head_dim, int page_size, int mask_mode,
+                             int sink_tokens, int window_tokens, float sm_scale, int num_cus,
+                             int32_t* plan_blob_h, int64_t blob_capacity_ints,
+                             bsx_attn_plan_t* out) {
+  PLAN_REQUIRE(qo_indptr_h && kv_indptr_h && kv_last_page_len_h && plan_blob_h && out,
+               BSX_ERR_INVALID, "null argument to bsx_attn_plan");
+  PLAN_REQUIRE(batch >= 0, BSX_ERR_INVALID, "batch must be >= 0 (got %d)", batch);
+  PLAN_REQUIRE(num_kv_heads > 0 && num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0,
+               BSX_ERR_INVALID, "num_qo_heads (%d) must be a positive multiple of num_kv_heads (%d)",
+               num_qo_heads, num_kv_heads);
+  PLAN_REQUIRE(head_dim == 64 || head_dim == 128, BSX_ERR_UNSUPPORTED,
+               "head_dim %d not supported (64 or 128)", head_dim);
+  PLAN_REQUIRE(page_size >= 1 && page_size <= 1024 && (page_size & (page_size - 1)) == 0,
+               BSX_ERR_UNSUPPORTED, "page_size %d must be a power of two <= 1024", page_size);
+  PLAN_REQUIRE(mask_mode >= BSX_MASK_NONE && mask_mode <= BSX_MASK_STREAMING, BSX_ERR_INVALID,
+               "unknown mask mode %d", mask_mode);
+  PLAN_REQUIRE(num_cus >= 1, BSX_ERR_INVALID, "num_cus must be >= 1");
+  PLAN_REQUIRE(mask_mode != BSX_MASK_STREAMING || (sink_tokens >= 0 && window_tokens >= 0),
+               BSX_ERR_INVALID, "streaming view needs sink >= 0 and window >= 0");
+  PLAN_REQUIRE(qo_indptr_h[0] == 0 && kv_indptr_h[0] == 0, BSX_ERR_INVALID,
+               "qo_indptr[0] and paged_kv_indptr[0] must be 0");
+
+  const int group = num_qo_heads / num_kv_heads;
+  std::vector<int32_t> qo_len(batch), kv_len(batch);
+  int max_qo = 0;
+  for (int b = 0; b < batch; ++b) {
+    const int q = qo_indptr_h[b + 1] - qo_indptr_h[b];
+    const int np = kv_indptr_h[b + 1] - kv_indptr_h[b];
+    const int last = kv_last_page_len_h[b];
+    PLAN_REQUIRE(q >= 0, BSX_ERR_INVALID, "qo_indptr not non-decreasing at request %d", b);
+    PLAN_REQUIRE(np >= 0, BSX_ERR_INVALID, "paged_kv_indptr not non-decreasing at request %d", b);
+    PLAN_REQUIRE(last >= 0 && last <= page_size, BSX_ERR_INVALID,
+                 "paged_kv_last_page_len[%d] = %d outside [0, page_size=%d]", b, last, page_size);
+    const int64_t kl = np > 0 ? (int64_t)(np - 1) * page_size + last : 0;
+    PLAN_REQUIRE(kl < (1LL << 30), BSX_ERR_UNSUPPORTED, "kv length too large at request %d", b);
+    qo_len[b] = q;
+    kv_len[b] = (int32_t)kl;
+    if (mask_mode == BSX_MASK_TREE)
+      PLAN_REQUIRE(q <= 32, BSX_ERR_UNSUPPORTED,
+                   "tree mask supports at most 32 query tokens per request (request %d has %d)", b,
+                   q);
+    max_qo = std::max(max_qo, q);
+  }
+
+  // Query rows per kv head = qo_len * group.  A wave covers 16 or 32 of them.
+  const int64_t max_rows = (int64_t)max_qo * group;
+  const int qrow_tile = max_rows <= 16 ? 16 : 32;
+  const int qrow_blocks = (int)std::max<int64_t>(1, (max_rows + qrow_tile - 1) / qrow_tile);
+  int hpc = 1;  // kv heads per workgroup: largest divisor of num_kv_heads that fits
+  for (int c = 1; c <= num_kv_heads; ++c)
+    if (num_kv_heads % c == 0 && c * std::min(qrow_blocks, kMaxWavesPerCta) <= kMaxWavesPerCta)
+      hpc = c;
+  // Waves of one workgroup (the run side splits query blocks the same way).
+  int qbpc = qrow_blocks;
+  while (qbpc * hpc > kMaxWavesPerCta) qbpc = (qbpc + 1) / 2;
+  const int n_qgroups = (qrow_blocks + qbpc - 1) / qbpc;
+  const int cta_waves = hpc * qbpc;
+  // One grid row (blockIdx.y) per (kv-head group, query group); size grid.x so that
+  // all workgroups are resident at once on num_cus compute units (4 SIMDs each).
+  const int grid_y = (num_kv_heads / hpc) * n_qgroups;
+  const int resident_per_cu = std::max(1, 4 * waves_per_simd(head_dim, qrow_tile) / cta_waves);
+  const int num_ctas = std::max(1, (num_cus * resident_per_cu) / grid_y);
+
+  // Work units: contiguous tile ranges per request (two for the sink+window view).
+  std::vector<Unit> units;
+  units.reserve(2 * (size_t)batch);
+  std::vector<int> units_of(batch, 0);
+  int64_t total = 0;
+  for (int b = 0; b < batch; ++b) {
+    if (qo_len[b] == 0) continue;
+    const int ntiles = (kv_len[b] + kTileTokens - 1) / kTileTokens;
+    if (mask_mode == BSX_MASK_STREAMING && kv_len[b] > sink_tokens + window_tokens) {
+      const int a_end = (sink_tokens + kTileTokens - 1) / kTileTokens;
+      const int w_beg = std::max(0, (kv_len[b] - window_tokens)) / kTileTokens;
+      if (w_beg <= a_end) {
+        units.push_back({b, 0, ntiles});
+      } else {
+        if (a_end > 0) units.push_back({b, 0, a_end});
+        units.push_back({b, w_beg, ntiles});
+      }
+    } else {
+      units.push_back({b, 0, ntiles});
+    }
+  }
+  for (const Unit& u : units) total += std::max(1, u.te - u.tb);  // empty range still writes zeros
+
+  const int W = (int)std::max<int64_t>(1, std::min<int64_t>(num_ctas, std::max<int64_t>(total, 1)));
+
+  // Cut the virtual tile sequence into W equal shares (floor(w*T/W) boundaries).
+  struct Seg {
+    int b, tb, te;
+  };
+  std::vector<std::vector<Seg>> per_cta(W);
+  {
+    auto share_start = [&](int w) -> int64_t { return w >= W ? total : (total * w) / W; };
+    int64_t pos = 0;  // virtual position where the current unit starts
+    int w = 0;
+    for (const Unit& u : units) {
+      const int64_t cost = std::max(1, u.te - u.tb);
+      int64_t a = pos;
+      const int64_t e = pos + cost;
+      while (a < e) {
+        while (share_start(w + 1) <= a) ++w;
+        const int64_t cut = std::min(e, share_start(w + 1));
+        if (u.te == u.tb)
+          per_cta[w].push_back({u.b, u.tb, u.te});
+        else
+          per_cta[w].push_back({u.b, u.tb + (int)(a - pos), u.tb + (int)(cut - pos)});
+        a = cut;
+      }
+      pos = e;
+    }
+  }
+  for (int w = 0; w < W; ++w)
+    for (const Seg& s : per_cta[w]) units_of[s.b]++;
+
+  // Partial slots for requests that ended up in more than one segment.
+  std::vector<int32_t> part_indptr(batch + 1, 0);
+  std::vector<int32_t> merge_seqs;
+  for (int b = 0; b < batch; ++b) {
+    part_indptr[b + 1] = part_indptr[b] + (units_of[b] > 1 ? units_of[b] : 0);
+    if (units_of[b] > 1) merge_seqs.push_back(b);
+  }
+  const int num_partials = part_indptr[batch];
+  std::vector<int32_t> next_slot(part_indptr.begin(), part_indptr.end() - 1);
+
+  int nseg = 0;
+  for (int w = 0; w < W; ++w) nseg += (int)per_cta[w].size();
+
+  const int64_t need = 4LL * batch + (W + 1) + 4LL * nseg + (int64_t)merge_seqs.size() + (batch + 1);
+  PLAN_REQUIRE(need <= blob_capacity_ints, BSX_ERR_CAPACITY,
+               "plan blob needs %lld int32 entries, capacity %lld", (long long)need,
+               (long long)blob_capacity_ints);
+
+  int32_t* blob = plan_blob_h;
+  const int off_seq = 0;
+  const int off_seg_indptr = off_seq + 4 * batch;
+  const int off_segments = off_seg_indptr + W + 1;
+  const int off_merge = off_segments + 4 * nseg;
+  const int off_part = off_merge + (int)merge_seqs.size();
+  for (int b = 0; b < batch; ++b) {
+    blob[off_seq + 4 * b + 0] = qo_indptr_h[b];
+    blob[off_seq + 4 * b + 1] = qo_len[b];
+    blob[off_seq + 4 * b + 2] = kv_len[b];
+    blob[off_seq + 4 * b + 3] = kv_indptr_h[b];
+  }
+  int si = 0;
+  for (int w = 0; w < W; ++w) {
+    blob[off_seg_indptr + w] = si;
+    for (const Seg& s : per_cta[w]) {
+      blob[off_segments + 4 * si + 0] = s.b;
+      blob[off_segments + 4 * si + 1] = s.tb;
+      blob[off_segments + 4 * si + 2] = s.te;
+      blob[off_segments + 4 * si + 3] = units_of[s.b] > 1 ? next_slot[s.b]++ : -1;
+      ++si;
+    }
+  }
+  blob[off_seg_indptr + W] = si;
+  for (size_t i = 0; i < merge_seqs.size(); ++i) blob[off_merge + (int)i] = merge_seqs[i];
+  for (int b = 0; b <= batch; ++b) blob[off_part + b] = part_indptr[b];
+
+  memset(out, 0, sizeof(*out));
+  out->batch = batch;
+  out->num_qo_heads = num_qo_heads;
+  out->num_kv_heads = num_kv_heads;
+  out->head_dim = head_dim;
+  out->page_size = page_size;
+  out->mask_mode = mask_mode;
+  out->group_size = group;
+  out->qrow_tile = qrow_tile;
+  out->qrow_blocks = qrow_blocks;
+  out->heads_per_cta = hpc;
+  out->qblocks_per_cta = qbpc;
+  out->num_qgroups = n_qgroups;
+  out->num_ctas = W;
+  out->num_segments = nseg;
+  out->num_partials = num_partials;
+  out->num_merge_seqs = (int)merge_seqs.size();
+  out->max_qo_len = max_qo;
+  out->tile_tokens = kTileTokens;
+  out->sink_tokens = sink_tokens;
+  out->window_tokens = window_tokens;
+  out->off_seq = off_seq;
+  out->off_seg_indptr = off_seg_indptr;
+  out->off_segments = off_segments;
+  out->off_merge_seqs = off_merge;
+  out->off_part_indptr = off_part;
+  out->plan_ints = (int32_t)need;
+  const int64_t rows_total = (int64_t)qrow_tile * qrow_blocks;
+  out->float_ws_bytes = (int64_t)num_partials * num_kv_heads * rows_total * (head_dim + 1) * 4;
+  out->sm_scale = sm_scale > 0.f ? sm_scale : 1.0f / std::sqrt((float)head_dim);
+  out->total_qo = batch > 0 ? qo_indptr_h[batch] : 0;
+  return BSX_OK;
+}

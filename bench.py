@@ -1,0 +1,251 @@
+"""Benchmark of the speculative-verification hot path on one MI355X.
+
+Workload: Llama-3-8B shaped verify step of one decoder layer —
+B=64 requests, context 1k-4k, k=4 chain draft (5 query tokens, causal), 32 query /
+8 kv heads, head_dim 128, page size 16, random page permutation, bf16, values
+N(0,1)*0.5 — i.e. the paged append of the 5 new K/V rows per request followed by
+verify attention.  A "step" is append + attention over the whole batch; three
+independent input sets rotate so the 256 MB last-level cache cannot serve repeats.
+
+Printed: one JSON line with
+  value       verify-attention HBM GB/s (algorithmic bytes / kernel time)
+  roofline    against the 8 TB/s HBM peak, from hipEvent timing of run()
+  accepted_tok_s  accepted tokens/s of a 32-layer verify step: 32 x (append +
+              attention) + fused greedy acceptance over [64, 5, 128256] bf16 logits
+              (draft = target argmax with probability 0.7), reference acceptance rule
+  stochastic_accept  config 5 (B=128, k=5, V=128256, bf16): time and HBM fraction
+  cpu_baseline    the fp32 CPU oracle on a bounded sample of the same workload
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "verify-attn HBM GB/s (% of 8 TB/s) + accepted tok/s, Llama-8B shape B=64 k=4"
+
+
+def attn_bytes(b) -> int:
+    """Algorithmic bytes of one verify-attention pass: every K/V row of every request
+    once, Q, O, page ids (and mask words) once."""
+    import numpy as np
+    kv_tokens = int(np.sum(b.kv_lens))
+    nnz = b.q.shape[0]
+    kv = kv_tokens * b.num_kv_heads * b.head_dim * 2 * 2
+    qo = 2 * nnz * b.num_qo_heads * b.head_dim * 2
+    pages = int(b.kv_indptr[-1].item()) * 4
+    words = 0 if b.mask_words is None else nnz * 4
+    return kv + qo + pages + words
+
+
+def append_bytes(b) -> int:
+    nnz = b.k_new.shape[0]
+    return 2 * (2 * nnz * b.num_kv_heads * b.head_dim * 2)
+
+
+def time_events(fn, iters: int, warmup: int):
+    import torch
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for i in range(iters):
+        starts[i].record()
+        fn(i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]  # microseconds
+
+
+def median(xs):
+    s = sorted(xs)
+    return s[len(s) // 2]
+
+
+def cpu_baseline(sets, budget_s: float = 20.0):
+    """fp32 oracle (numpy) on a bounded sample: the first requests of the config-2 batch
+    until ~budget_s of CPU work; reported in the metric's unit (GB/s)."""
+    import numpy as np
+    import torch
+    from oracle import attention as OA
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:
+        cores = 1
+    b = sets[0]
+    q = b.q.float().cpu().numpy()
+    qo = b.qo_indptr.cpu().numpy()
+    kvp = b.kv_indptr.cpu().numpy()
+    idx = b.kv_indices.cpu().numpy()
+    last = b.kv_last_page_len.cpu().numpy()
+    lens = b.kv_lens
+    t_total, done_bytes, n_req = 0.0, 0, 0
+    B = len(qo) - 1
+    while t_total < budget_s and n_req < B:
+        r = n_req
+        pages = idx[kvp[r]:kvp[r + 1]]
+        sub = b.cache[torch.from_numpy(pages.astype(np.int64)).to(b.cache.device)].float().cpu().numpy()
+        t0 = time.perf_counter()
+        OA.verify_attention(q[qo[r]:qo[r + 1]], sub, [0, qo[r + 1] - qo[r]],
+                            [0, len(pages)], np.arange(len(pages), dtype=np.int32),
+                            last[r:r + 1], b.page_size, mode="causal")
+        t_total += time.perf_counter() - t0
+        done_bytes += (int(lens[r]) * b.num_kv_heads * b.head_dim * 4
+                       + 2 * (qo[r + 1] - qo[r]) * b.num_qo_heads * b.head_dim * 2 + len(pages) * 4)
+        n_req += 1
+    return {"value": round(done_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": int(cores),
+            "kind": "port",
+            "sample": f"{n_req} of {B} config-2 requests, fp32 numpy paged gather + softmax "
+                      f"attention ({t_total:.1f} s)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-accept", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the "
+              "verify path shards by request / kv head with no exchange, see the design notes.",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import batchspec_amd as bsx
+    from batchspec_amd.workloads import config2, greedy_case, stochastic_case
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    print("bench: building 3 config-2 input sets on the GPU", file=sys.stderr, flush=True)
+    sets = [config2(device=dev, seed=1002 + i) for i in range(3)]
+    ws = [torch.empty(256 << 20, dtype=torch.uint8, device=dev) for _ in sets]
+    wrappers = []
+    plan_us = []
+    for b, w_buf in zip(sets, ws):
+        w = bsx.BatchPrefillWithPagedKVCacheWrapper(w_buf, "NHD")
+        t0 = time.perf_counter()
+        w.plan(b.qo_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, b.num_qo_heads,
+               b.num_kv_heads, b.head_dim, b.page_size, causal=True, q_data_type=torch.bfloat16)
+        plan_us.append((time.perf_counter() - t0) * 1e6)
+        wrappers.append(w)
+    outs = [torch.empty_like(b.q) for b in sets]
+    abytes = [attn_bytes(b) for b in sets]
+    pbytes = [append_bytes(b) for b in sets]
+
+    def step(i):
+        j = i % 3
+        b = sets[j]
+        bsx.append_kv(b.k_new, b.v_new, b.qo_indptr, b.cache, b.kv_indptr, b.kv_indices,
+                      b.kv_last_page_len)
+        wrappers[j].run(b.q, b.cache, out=outs[j])
+
+    # --- timed steps (append + attention), whole-loop clock
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(args.steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    step_bytes = sum(abytes[i % 3] + pbytes[i % 3] for i in range(args.steps)) / args.steps
+
+    # --- per-launch hipEvent timing of attention run() and of the append
+    attn_us = time_events(lambda i: wrappers[i % 3].run(sets[i % 3].q, sets[i % 3].cache,
+                                                        out=outs[i % 3]), args.steps, 3)
+    app_us = time_events(lambda i: bsx.append_kv(sets[i % 3].k_new, sets[i % 3].v_new,
+                                                 sets[i % 3].qo_indptr, sets[i % 3].cache,
+                                                 sets[i % 3].kv_indptr, sets[i % 3].kv_indices,
+                                                 sets[i % 3].kv_last_page_len), args.steps, 3)
+    t_attn = sum(attn_us) / len(attn_us)
+    t_app = sum(app_us) / len(app_us)
+    a_bytes = sum(abytes) / 3
+    achieved = a_bytes / (t_attn * 1e-6) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config2: Llama-3-8B verify layer, B=64, ctx U[1024,4096], "
+                               "k=4 (5 causal queries), 32/8 heads, D=128, page 16, random "
+                               "page permutation, bf16; step = paged append + verify attention",
+                   "batch": 64, "draft_len": 4, "num_qo_heads": 32, "num_kv_heads": 8,
+                   "head_dim": 128, "page_size": 16},
+        "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
+        "step_gbs": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "attn_us": round(t_attn, 2),
+        "attn_us_median": round(median(attn_us), 2),
+        "append_us": round(t_app, 2),
+        "attn_bytes": int(a_bytes),
+        "plan_us": round(median(plan_us), 1),
+        "wall_s": round(wall, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+
+    if not args.skip_accept:
+        # greedy acceptance at the config-2 shape: fused argmax over [64, 5, 128256] bf16
+        g = greedy_case(B=64, k=4, V=128256, p_match=0.7, seed=2002, dtype=torch.bfloat16)
+        gl, gd = g.target_logits.to(dev), g.draft_tokens.to(dev)
+        acc_us = time_events(lambda i: bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1),
+                             args.steps, 3)
+        _, acc_ref, _ = bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1)
+        _, acc_pre, _ = bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1,
+                                               accept_rule="prefix")
+        t_acc = sum(acc_us) / len(acc_us)
+        t_model = 32 * (t_attn + t_app) + t_acc
+        n_ref, n_pre = int(acc_ref.sum()), int(acc_pre.sum())
+        result["accepted_tok_s"] = round(n_ref / (t_model * 1e-6), 1)
+        result["accepted_tok_s_prefix_rule"] = round(n_pre / (t_model * 1e-6), 1)
+        result["mean_accept_len"] = {"reference_rule": n_ref / 64, "prefix_rule": n_pre / 64}
+        gbytes = gl.numel() * 2
+        result["greedy_accept"] = {"us": round(t_acc, 2), "GB/s": round(gbytes / t_acc / 1e3, 1),
+                                   "frac": round(gbytes / t_acc / 1e3 / HBM_PEAK_GBS, 4)}
+        result["verify_step_32_layers_us"] = round(t_model, 1)
+        del gl, g
+        # stochastic acceptance (config 5)
+        s = stochastic_case(device=dev)
+        st_us = time_events(lambda i: bsx.sampling.chain_speculative_sampling_from_logits(
+            s.draft_logits, s.draft_tokens, s.target_logits, 1.0, uniforms=s.uniforms),
+            max(5, args.steps // 3), 2)
+        t_st = sum(st_us) / len(st_us)
+        sbytes = (s.target_logits.numel() + s.draft_logits.numel()) * 2
+        result["stochastic_accept"] = {"us": round(t_st, 2), "GB/s": round(sbytes / t_st / 1e3, 1),
+                                       "frac": round(sbytes / t_st / 1e3 / HBM_PEAK_GBS, 4),
+                                       "bytes": sbytes}
+        del s
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(sets)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,242 @@
+/*
+ * bsx.h — C ABI of the MI355X (gfx950) speculative-verification hot path.
+ *
+ * Three pieces, each replacing one FlashInfer call site of BatchSpec:
+ *   1. paged-KV verify attention  (BatchPrefillWithPagedKVCacheWrapper.plan/run)
+ *   2. paged KV append            (get_seq_lens / get_batch_indices_positions /
+ *                                   append_paged_kv_cache)
+ *   3. speculative acceptance     (evaluate_posterior greedy branch,
+ *                                   chain_speculative_sampling, sampling.softmax)
+ *
+ * Conventions
+ *   - Every pointer named *_d is device memory; *_h is host memory.
+ *   - The caller owns every buffer, including workspaces; the library never
+ *     allocates device memory.
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *     Every device entry point is asynchronous, does no host synchronisation and
+ *     may be captured into a hipGraph.
+ *   - Every entry point returns a bsx_status; on failure bsx_last_error() gives a
+ *     thread-local message. Nothing throws across the ABI.
+ *   - Integer index tensors are int32 (CSR page tables) or int64 (token ids), as
+ *     in the reference.
+ */
+#ifndef BSX_H
+#define BSX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  BSX_OK = 0,
+  BSX_ERR_INVALID = -1,     /* bad argument (shape, dtype, null pointer)        */
+  BSX_ERR_CAPACITY = -2,    /* caller buffer or workspace too small             */
+  BSX_ERR_UNSUPPORTED = -3, /* valid request outside what the kernels implement */
+  BSX_ERR_HIP = -4          /* a HIP runtime call failed                        */
+} bsx_status;
+
+enum { BSX_DTYPE_BF16 = 0, BSX_DTYPE_FP16 = 1, BSX_DTYPE_FP32 = 2 };
+
+/* Attention mask modes (the reference's plan(causal=..., custom_mask=...)). */
+enum {
+  BSX_MASK_NONE = 0,   /* full attention to all kv_len tokens                   */
+  BSX_MASK_CAUSAL = 1, /* bottom-right aligned causal: q row t sees
+                          j <= kv_len - qo_len + t                             */
+  BSX_MASK_TREE = 2,   /* full attention to the first kv_len - qo_len tokens,
+                          then bit (j - (kv_len - qo_len)) of a per-query-token
+                          uint32 word over the last qo_len tokens (qo_len <= 32) */
+  BSX_MASK_STREAMING = 3 /* sink + recent window view: token j is visible iff
+                          j < sink or j >= kv_len - window, combined with the
+                          causal rule over the last qo_len tokens              */
+};
+
+const char* bsx_last_error(void);
+int bsx_version(void);
+
+/* ------------------------------------------------------------------------- */
+/* 1. Verify attention                                                        */
+/* ------------------------------------------------------------------------- */
+
+/* Host-side schedule produced by bsx_attn_plan; the device half of the plan is
+ * an int32 blob of `plan_ints` entries that the caller copies to device memory
+ * (any stream ordering that completes before bsx_attn_run reads it). */
+typedef struct {
+  int32_t batch;
+  int32_t num_qo_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t page_size;
+  int32_t mask_mode;
+  int32_t group_size;     /* num_qo_heads / num_kv_heads                      */
+  int32_t qrow_tile;      /* query rows per wave (16 or 32)                   */
+  int32_t qrow_blocks;    /* waves per kv head that split the query rows      */
+  int32_t heads_per_cta;  /* kv heads handled by one workgroup                */
+  int32_t qblocks_per_cta;/* query-row blocks handled by one workgroup        */
+  int32_t num_qgroups;    /* ceil(qrow_blocks / qblocks_per_cta)              */
+  int32_t num_ctas;       /* grid.x of the main kernel; grid.y =
+                             (num_kv_heads/heads_per_cta) * num_qgroups       */
+  int32_t num_segments;
+  int32_t num_partials;   /* partial-result slots that need merging           */
+  int32_t num_merge_seqs; /* sequences whose kv range was split               */
+  int32_t max_qo_len;
+  int32_t tile_tokens;    /* kv tokens per inner-loop tile (32)               */
+  int32_t sink_tokens;    /* BSX_MASK_STREAMING only                          */
+  int32_t window_tokens;  /* BSX_MASK_STREAMING only                          */
+  int32_t off_seq;        /* int32 offsets of the sub-arrays inside the blob   */
+  int32_t off_seg_indptr;
+  int32_t off_segments;
+  int32_t off_merge_seqs;
+  int32_t off_part_indptr;
+  int32_t plan_ints;      /* total int32 entries of the device blob           */
+  int64_t float_ws_bytes; /* bytes of float workspace bsx_attn_run needs       */
+  float sm_scale;
+  int32_t total_qo;       /* qo_indptr[batch]                                 */
+} bsx_attn_plan_t;
+
+/* Size (int32 entries) of the host buffer bsx_attn_plan needs for its blob. */
+int64_t bsx_attn_plan_ints_bound(int batch, int num_cus);
+
+/* Replaces BatchPrefillWithPagedKVCacheWrapper.plan(...) as called by
+ * batchspec/backends/standard_engine.py:132-143 (causal=True) and
+ * batchspec/backends/mtp_engine.py:420-432 (custom mask): validates the page
+ * table, derives kv lengths (reference formula of FlashInfer get_seq_lens used at
+ * batchspec/models/modules/kv_cache.py:66-70), and splits the kv work evenly over
+ * a persistent grid sized to fill `num_cus` compute units.  Host-only; no GPU
+ * needed.
+ *   qo_indptr_h[batch+1], kv_indptr_h[batch+1], kv_last_page_len_h[batch]
+ *   sm_scale <= 0 means 1/sqrt(head_dim). */
+int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                  const int32_t* kv_last_page_len_h, int batch, int num_qo_heads,
+                  int num_kv_heads, int head_dim, int page_size, int mask_mode,
+                  int sink_tokens, int window_tokens, float sm_scale, int num_cus,
+                  int32_t* plan_blob_h, int64_t blob_capacity_ints,
+                  bsx_attn_plan_t* plan_out);
+
+/* Replaces BatchPrefillWithPagedKVCacheWrapper.run(q, paged_kv_cache) as called
+ * at batchspec/models/modules/attention/standard.py:69.
+ *   q_d        [total_qo, num_qo_heads, head_dim] (bf16 or fp16), row stride
+ *              q_stride_tok elements between tokens
+ *   k_cache_d  K of page p, slot s, head h at
+ *              k_cache_d + p*page_stride + s*num_kv_heads*head_dim + h*head_dim
+ *   v_cache_d  same addressing (for the reference layout [P,2,ps,H,D],
+ *              v_cache_d = k_cache_d + ps*H*D and page_stride = 2*ps*H*D)
+ *   kv_indices_d page ids in CSR order (paged_kv_indices)
+ *   mask_words_d uint32 per query token for BSX_MASK_TREE, else NULL
+ *   out_d      [total_qo, num_qo_heads, head_dim], same dtype as q
+ *   lse_d      optional float [total_qo, num_qo_heads] log-sum-exp (natural
+ *              log, of the scaled scores), or NULL
+ *   float_ws_d at least plan->float_ws_bytes bytes */
+int bsx_attn_run(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d,
+                 void* float_ws_d, int dtype, const void* q_d, int64_t q_stride_tok,
+                 const void* k_cache_d, const void* v_cache_d, int64_t page_stride,
+                 const int32_t* kv_indices_d, const uint32_t* mask_words_d,
+                 void* out_d, int64_t out_stride_tok, float* lse_d, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* 2. Paged KV append                                                         */
+/* ------------------------------------------------------------------------- */
+
+/* FlashInfer get_seq_lens as used at batchspec/models/modules/kv_cache.py:66-70:
+ * seq_lens[b] = (kv_indptr[b+1]-kv_indptr[b]-1)*page_size + last_page_len[b]
+ * (0 when the request holds no page). */
+int bsx_get_seq_lens(const int32_t* kv_indptr_d, const int32_t* kv_last_page_len_d,
+                     int batch, int page_size, int32_t* seq_lens_d, void* stream);
+
+/* FlashInfer get_batch_indices_positions as used at
+ * batchspec/models/modules/kv_cache.py:64-72: for token i of request b,
+ * batch_indices[i] = b, positions[i] = seq_lens[b] - n_b + (i - append_indptr[b]). */
+int bsx_get_batch_indices_positions(const int32_t* append_indptr_d,
+                                    const int32_t* seq_lens_d, int batch, int nnz,
+                                    int32_t* batch_indices_d, int32_t* positions_d,
+                                    void* stream);
+
+/* FlashInfer append_paged_kv_cache (kv_layout NHD) as used at
+ * batchspec/models/modules/kv_cache.py:73-83: cache[page(pos), slot(pos)] = k[i]. */
+int bsx_append_paged_kv_cache(const void* append_key_d, const void* append_value_d,
+                              int64_t key_stride_tok, int64_t value_stride_tok,
+                              const int32_t* batch_indices_d, const int32_t* positions_d,
+                              int nnz, void* k_cache_d, void* v_cache_d,
+                              int64_t page_stride, const int32_t* kv_indices_d,
+                              const int32_t* kv_indptr_d, int num_kv_heads, int head_dim,
+                              int page_size, int elem_bytes, void* stream);
+
+/* Fused StandardKVCache.update (batchspec/models/modules/kv_cache.py:47-84): the
+ * three calls above in one kernel, without the host read of append_indptr[-1]
+ * (kv_cache.py:71); nnz comes from the shape of k. */
+int bsx_kv_append(const void* k_d, const void* v_d, int64_t k_stride_tok,
+                  int64_t v_stride_tok, const int32_t* append_indptr_d,
+                  const int32_t* kv_indptr_d, const int32_t* kv_indices_d,
+                  const int32_t* kv_last_page_len_d, int batch, int nnz, void* k_cache_d,
+                  void* v_cache_d, int64_t page_stride, int num_kv_heads, int head_dim,
+                  int page_size, int elem_bytes, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* 3. Acceptance                                                              */
+/* ------------------------------------------------------------------------- */
+
+/* Row argmax (torch.argmax: first maximum, NaN counts as maximum) over
+ * [rows, vocab] logits, as used by `target_logits.argmax(-1)` at
+ * batchspec/backends/mtp_engine.py:747 and greedy `sample` at
+ * batchspec/backends/utils/sampling.py:89-90.  ws_d: bsx_argmax_ws_bytes. */
+int64_t bsx_argmax_ws_bytes(int64_t rows, int64_t vocab);
+int bsx_argmax(const void* logits_d, int dtype, int64_t rows, int64_t vocab,
+               int64_t row_stride, int64_t* out_d, void* ws_d, int64_t ws_bytes,
+               void* stream);
+
+/* Greedy branch of MTPEngine.evaluate_posterior
+ * (batchspec/backends/mtp_engine.py:553-560).
+ *   draft_d [B,k] int64; target ids: target_ids_d [B,k+1] int64, or (when
+ *   target_ids_d is NULL) target_logits_d [B,k+1,V] whose argmax is fused.
+ *   mode 0 = reference rule accept = (#matches)+1 (mtp_engine.py:556);
+ *   mode 1 = longest-prefix rule.
+ *   Outputs: bonus_d [B] int64, accept_d [B] int64, eos_acc_d [B] uint8. */
+int64_t bsx_accept_greedy_ws_bytes(int B, int k, int64_t vocab);
+int bsx_accept_greedy(const int64_t* draft_d, const int64_t* target_ids_d,
+                      const void* target_logits_d, int dtype, int B, int k,
+                      int64_t vocab, int64_t eos_id, int mode, int64_t* bonus_d,
+                      int64_t* accept_d, uint8_t* eos_acc_d, void* ws_d,
+                      int64_t ws_bytes, void* stream);
+
+/* Chain speculative sampling (flashinfer.sampling.chain_speculative_sampling as
+ * called at batchspec/backends/mtp_engine.py:569) with explicit uniforms.
+ *   draft_probs_d [B,k,V] fp32 or NULL (NULL = one-hot at the draft token, the
+ *   MTP case of mtp_engine.py:565-567); target_probs_d [B,k+1,V] fp32;
+ *   draft_ids_d [B,k] int64; uniforms_d [B,k+1] fp32 in [0,1): u[:, i<k] for the
+ *   ratio tests, u[:, k] for the residual / bonus draw.
+ *   Outputs: out_ids_d [B,k+1] int32 (-1 padded), accepted_d [B] int32 (draft
+ *   tokens accepted when each position is tested on its own), emitted_d [B] int32
+ *   (length of the accepted prefix). */
+int64_t bsx_chain_ws_bytes(int B, int k, int64_t vocab);
+int bsx_chain_speculative_sampling(const float* draft_probs_d, const int64_t* draft_ids_d,
+                                   const float* target_probs_d, const float* uniforms_d,
+                                   int B, int k, int64_t vocab, int32_t* out_ids_d,
+                                   int32_t* accepted_d, int32_t* emitted_d, void* ws_d,
+                                   int64_t ws_bytes, void* stream);
+
+/* Same test fused with the temperature softmax of both distributions
+ * (get_sampling_probs, batchspec/backends/utils/sampling.py:47-48, with top-k
+ * and top-p off): reads bf16/fp16/fp32 logits once instead of fp32 probs.
+ *   draft_logits_d [B,k,V] or NULL (one-hot draft); target_logits_d [B,k+1,V]. */
+int bsx_chain_speculative_sampling_logits(const void* draft_logits_d,
+                                          const int64_t* draft_ids_d,
+                                          const void* target_logits_d, int dtype,
+                                          float temperature, const float* uniforms_d,
+                                          int B, int k, int64_t vocab, int32_t* out_ids_d,
+                                          int32_t* accepted_d, int32_t* emitted_d,
+                                          void* ws_d, int64_t ws_bytes, void* stream);
+
+/* flashinfer.sampling.softmax(logits, temperature) as called at
+ * batchspec/backends/utils/sampling.py:48, with the deterministic reduction
+ * order shared with the fused acceptance kernels. probs_d [rows, vocab] fp32. */
+int64_t bsx_softmax_ws_bytes(int64_t rows);
+int bsx_softmax(const void* logits_d, int dtype, float temperature, int64_t rows,
+                int64_t vocab, float* probs_d, void* ws_d, int64_t ws_bytes,
+                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BSX_H */

@@ -1,0 +1,206 @@
+"""CPU tests of the drop-in boundary: the C-ABI library loads and exports every symbol
+of include/bsx.h; the host planner's schedule is valid; the host-side mirrors
+(page table, masks, custom-mask packing) match the oracle; the product refuses CPU
+tensors instead of falling back."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import batchspec_amd as bsx
+from batchspec_amd import _lib, masks
+from batchspec_amd.attention import custom_mask_to_tree_words
+from oracle import masks as OM
+from oracle import paging as OP
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_functions():
+    text = (ROOT / "include" / "bsx.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bsx_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol(bsx):
+    names = header_functions()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(bsx, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes bindings must match the header"
+    assert bsx.bsx_version() == 1
+
+
+def _plan(qo, kvp, last, Hq=32, Hkv=8, D=128, ps=16, mode=_lib.MASK_CAUSAL, cus=256, sink=0,
+          window=0):
+    L = _lib.load()
+    qo, kvp, last = (np.ascontiguousarray(a, dtype=np.int32) for a in (qo, kvp, last))
+    B = len(qo) - 1
+    bound = L.bsx_attn_plan_ints_bound(B, cus)
+    blob = np.zeros(bound, np.int32)
+    plan = _lib.AttnPlan()
+    rc = L.bsx_attn_plan(qo.ctypes.data, kvp.ctypes.data, last.ctypes.data, B, Hq, Hkv, D, ps, mode,
+                         sink, window, 0.0, cus, blob.ctypes.data, bound, ctypes.byref(plan))
+    _lib.check(rc, "plan")
+    return plan, blob
+
+
+def _segments(plan, blob):
+    segs = blob[plan.off_segments: plan.off_segments + 4 * plan.num_segments].reshape(-1, 4)
+    indptr = blob[plan.off_seg_indptr: plan.off_seg_indptr + plan.num_ctas + 1]
+    return segs, indptr
+
+
+@pytest.mark.parametrize("cus", [1, 7, 256])
+def test_plan_covers_every_tile_once_and_balances(cus):
+    rng = np.random.default_rng(cus)
+    B = 64
+    ctx = rng.integers(1024, 4097, size=B)
+    kv = ctx + 5
+    pages = -(-kv // 16)
+    kvp = np.concatenate([[0], np.cumsum(pages)])
+    qo = np.arange(B + 1) * 5
+    last = (kv - 1) % 16 + 1
+    plan, blob = _plan(qo, kvp, last, cus=cus)
+    segs, indptr = _segments(plan, blob)
+    assert plan.heads_per_cta * plan.qblocks_per_cta <= 8
+    assert np.all(np.diff(indptr) >= 0) and indptr[-1] == plan.num_segments
+    covered = {b: np.zeros(-(-int(kv[b]) // 32), int) for b in range(B)}
+    for b, t0, t1, slot in segs:
+        covered[b][t0:t1] += 1
+    assert all(np.all(c == 1) for c in covered.values())
+    load = np.add.reduceat(segs[:, 2] - segs[:, 1], indptr[:-1]) if plan.num_segments else []
+    assert max(load) - min(load) <= 1
+    # partial slots: contiguous per split request, unique
+    slots = segs[segs[:, 3] >= 0, 3]
+    assert len(set(slots.tolist())) == len(slots) == plan.num_partials
+    pip = blob[plan.off_part_indptr: plan.off_part_indptr + B + 1]
+    for b, t0, t1, slot in segs:
+        if slot >= 0:
+            assert pip[b] <= slot < pip[b + 1]
+        else:
+            assert pip[b] == pip[b + 1]
+
+
+def test_plan_empty_kv_and_empty_queries():
+    plan, blob = _plan([0, 3, 3, 5], [0, 1, 1, 2], [0, 0, 4])
+    segs, _ = _segments(plan, blob)
+    reqs = sorted(segs[:, 0].tolist())
+    assert reqs == [0, 2]  # request 1 has no queries; request 0 (kv_len 0) still writes zeros
+    assert all(s[1] == s[2] for s in segs if s[0] == 0)
+
+
+def test_plan_streaming_skips_middle_tiles():
+    kv = 5000
+    plan, blob = _plan([0, 1], [0, -(-kv // 16)], [(kv - 1) % 16 + 1], mode=_lib.MASK_STREAMING,
+                       sink=64, window=512, cus=4)
+    segs, _ = _segments(plan, blob)
+    tiles = sorted(t for s in segs for t in range(s[1], s[2]))
+    assert tiles == list(range(0, 2)) + list(range((kv - 512) // 32, -(-kv // 32)))
+
+
+@pytest.mark.parametrize("bad,exc", [
+    (dict(D=96), NotImplementedError),
+    (dict(Hq=30, Hkv=8), ValueError),
+    (dict(ps=12), NotImplementedError),
+])
+def test_plan_rejects_unsupported(bad, exc):
+    with pytest.raises(exc):
+        _plan([0, 5], [0, 1], [5], **bad)
+
+
+def test_plan_rejects_bad_page_table():
+    with pytest.raises(ValueError, match="last_page_len"):
+        _plan([0, 5], [0, 1], [17])
+    with pytest.raises(ValueError, match="non-decreasing"):
+        _plan([0, 5, 4], [0, 1, 2], [3, 3])
+    with pytest.raises(NotImplementedError, match="tree mask"):
+        _plan([0, 33], [0, 3], [16], mode=_lib.MASK_TREE)
+
+
+def test_page_table_mirror_matches_oracle():
+    rng = np.random.default_rng(7)
+    pt = bsx.PageTable(16, 4, 512, "cpu")
+    pt.clear_kv()
+    ref = OP.Pages(4, 512, 16)
+    ref.clear_kv()
+    for _ in range(150):
+        if rng.random() < 0.6:
+            d = rng.integers(0, 40, size=4)
+            pt.insert_kv(torch.from_numpy(d.astype(np.int32)))
+            ref.insert_kv(d)
+        else:
+            tot = np.array([ref.total(r) for r in range(4)])
+            d = np.minimum(rng.integers(0, 30, size=4), tot)
+            pt.delete_kv(torch.from_numpy(d.astype(np.int32)))
+            ref.delete_kv(d)
+        indptr, indices, last = ref.table()
+        np.testing.assert_array_equal(pt.paged_kv_indptr.numpy(), indptr)
+        np.testing.assert_array_equal(pt.paged_kv_indices.numpy(), indices)
+        np.testing.assert_array_equal(pt.paged_kv_last_page_len.numpy(), last)
+
+
+def test_page_manager_mirror_known_answers_and_errors():
+    pm = bsx.PageManager(2, 64, "cpu")
+    ids = pm.allocate(torch.tensor([1, 1], dtype=torch.int32))
+    assert ids.tolist() == [0, 64]
+    indptr, indices = pm.allocate(torch.tensor([1, 0], dtype=torch.int32),
+                                  torch.tensor([0, 64], dtype=torch.int32),
+                                  torch.tensor([0, 1, 2], dtype=torch.int32))
+    assert indptr.tolist() == [0, 2, 3] and indices.tolist() == [0, 1, 64]
+    indptr, indices = pm.free(torch.tensor([1, 0], dtype=torch.int32), indices, indptr)
+    assert indptr.tolist() == [0, 1, 2] and indices.tolist() == [0, 64]
+    with pytest.raises(RuntimeError):
+        pm.free(torch.tensor([0, 5], dtype=torch.int32), indices, indptr)
+    small = bsx.PageManager(1, 1, "cpu")
+    small.allocate(torch.tensor([1], dtype=torch.int32))
+    with pytest.raises(RuntimeError):
+        small.allocate(torch.tensor([1], dtype=torch.int32))
+
+
+@pytest.mark.parametrize("k", [1, 2, 4])
+def test_mtp_mask_mirror_matches_oracle(k):
+    m, pos = masks.mtp_attn_mask_and_position_ids(k)
+    rm, rpos = OM.mtp_mask(k)
+    np.testing.assert_array_equal(m.numpy(), rm)
+    np.testing.assert_array_equal(pos.numpy(), rpos)
+
+
+def test_tree_words_match_oracle_ancestor_mask():
+    from batchspec_amd.workloads import random_tree_parents
+    rng = np.random.default_rng(3)
+    for _ in range(20):
+        par = random_tree_parents(32, rng)
+        w, d = masks.tree_mask_words(par)
+        m, depth = OM.tree_ancestor_mask(par)
+        np.testing.assert_array_equal(masks.mask_to_words(torch.from_numpy(m)), w)
+        np.testing.assert_array_equal(d, depth)
+        assert depth.max() <= 6
+
+
+def test_custom_mask_packing_of_mtp_verify_mask():
+    k = 4
+    cachelens = [7, 0, 30]
+    flat = masks.mtp_verify_custom_mask(cachelens, k)
+    S = (k + 1) ** 2
+    words = custom_mask_to_tree_words(flat, np.full(3, S), np.array(cachelens) + S)
+    common, _ = masks.mtp_attn_mask_and_position_ids(k)
+    expect = np.tile(masks.mask_to_words(common), 3)
+    np.testing.assert_array_equal(words, expect)
+    bad = flat.clone()
+    bad[3] = False  # hide a prefix token of request 0
+    with pytest.raises(NotImplementedError):
+        custom_mask_to_tree_words(bad, np.full(3, S), np.array(cachelens) + S)
+
+
+def test_product_has_no_cpu_path():
+    x = torch.zeros(2, 8)
+    with pytest.raises(ValueError, match="no CPU path"):
+        bsx.sampling.argmax(x)
+    with pytest.raises(ValueError, match="no CPU path"):
+        bsx.get_seq_lens(torch.zeros(3, dtype=torch.int32), torch.zeros(2, dtype=torch.int32), 16)
+    with pytest.raises(ValueError, match="no CPU path"):
+        bsx.BatchPrefillWithPagedKVCacheWrapper(torch.empty(1024, dtype=torch.uint8))

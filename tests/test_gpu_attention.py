@@ -1,0 +1,239 @@
+"""GPU parity of verify attention (through the C ABI) against the fp32 oracle.
+
+Tolerance (bf16/fp16 inputs; the oracle sees the same rounded inputs in fp32):
+|gpu - oracle| <= 2e-2 + 2e-2 * |oracle|  — the bound BASELINE.json's north star sets.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import batchspec_amd as bsx
+from batchspec_amd import masks as M
+from batchspec_amd.workloads import config2, config3, config4, make_verify_batch
+from oracle import attention as OA
+
+pytestmark = pytest.mark.gpu
+ATOL = RTOL = 2e-2
+DEV = "cuda:0"
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def oracle_out(b, mode, **kw):
+    return OA.verify_attention(b.q.float().cpu().numpy(), b.cache.float().cpu().numpy(),
+                               b.qo_indptr.cpu().numpy(), b.kv_indptr.cpu().numpy(),
+                               b.kv_indices.cpu().numpy(), b.kv_last_page_len.cpu().numpy(),
+                               b.page_size, mode=mode, **kw)
+
+
+def run_gpu(b, causal=True, workspace_mb=256, **plan_kw):
+    ws = torch.empty(workspace_mb << 20, dtype=torch.uint8, device=DEV)
+    w = bsx.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    w.plan(b.qo_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, b.num_qo_heads,
+           b.num_kv_heads, b.head_dim, b.page_size, causal=causal, q_data_type=b.q.dtype, **plan_kw)
+    out = w.run(b.q, b.cache)
+    torch.cuda.synchronize()
+    return out, w
+
+
+def check(got, ref):
+    g = got.float().cpu().numpy()
+    assert np.isfinite(g).all()
+    err = np.abs(g - ref) - (ATOL + RTOL * np.abs(ref))
+    assert err.max() <= 0, f"max excess {err.max():.4g}, max abs err {np.abs(g - ref).max():.4g}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 8, 2), (128, 32, 8), (128, 8, 8), (64, 16, 2)])
+def test_causal_small(dtype, D, Hq, Hkv):
+    say(f"causal small dtype={dtype} D={D} H={Hq}/{Hkv}")
+    b = make_verify_batch(4, 64, 256, 5, Hq, Hkv, D, 16, dtype=dtype, seed=1001).to(DEV)
+    out, _ = run_gpu(b)
+    check(out, oracle_out(b, "causal"))
+
+
+def test_config1_shape_fp32_inputs_cast():
+    say("config1 inputs cast to bf16")
+    b = make_verify_batch(4, 64, 256, 5, 8, 2, 64, 16, dtype=torch.float32, seed=1001)
+    b.q, b.cache = b.q.to(torch.bfloat16), b.cache.to(torch.bfloat16)
+    b = b.to(DEV)
+    out, _ = run_gpu(b)
+    check(out, oracle_out(b, "causal"))
+
+
+@pytest.mark.parametrize("ps", [1, 8, 16, 32, 64])
+def test_page_sizes(ps):
+    say(f"page size {ps}")
+    b = make_verify_batch(5, 30, 300, 5, 32, 8, 128, ps, dtype=torch.bfloat16, seed=ps,
+                          extra_pages=7).to(DEV)
+    out, _ = run_gpu(b)
+    check(out, oracle_out(b, "causal"))
+
+
+@pytest.mark.parametrize("qo", [1, 3, 8, 16, 40])
+def test_query_lengths(qo):
+    say(f"qo={qo}")
+    b = make_verify_batch(6, 50, 900, qo, 32, 8, 128, 16, dtype=torch.bfloat16, seed=100 + qo).to(DEV)
+    out, _ = run_gpu(b)
+    check(out, oracle_out(b, "causal"))
+
+
+def test_ragged_mixed_batch_with_empty_requests():
+    say("ragged qo/ctx incl. qo=0 and kv=0")
+    qo = np.array([5, 0, 1, 17, 5, 2, 0, 5])
+    ctx = np.array([100, 40, 0, 700, 3000, 0, 5, 31])
+    b = make_verify_batch(8, 0, 0, 0, 32, 8, 128, 16, dtype=torch.bfloat16, seed=7, qo_lens=qo,
+                          ctx=ctx).to(DEV)
+    out, _ = run_gpu(b)
+    check(out, oracle_out(b, "causal"))
+
+
+def test_non_causal():
+    say("non-causal")
+    b = make_verify_batch(5, 10, 500, 5, 32, 8, 128, 16, dtype=torch.bfloat16, seed=3).to(DEV)
+    out, _ = run_gpu(b, causal=False)
+    check(out, oracle_out(b, "none"))
+
+
+def test_long_context_split_and_merge():
+    say("long context split/merge")
+    b = make_verify_batch(3, 20000, 40000, 5, 32, 8, 128, 16, dtype=torch.bfloat16, scale=0.5,
+                          seed=11).to(DEV)
+    out, w = run_gpu(b)
+    assert w.plan_info.num_merge_seqs == 3
+    check(out, oracle_out(b, "causal"))
+
+
+def test_lse_output():
+    say("lse")
+    b = make_verify_batch(4, 100, 3000, 5, 32, 8, 128, 16, dtype=torch.bfloat16, seed=5).to(DEV)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
+    w = bsx.BatchPrefillWithPagedKVCacheWrapper(ws)
+    w.plan(b.qo_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, 32, 8, 128, 16,
+           causal=True, q_data_type=torch.bfloat16)
+    out, lse = w.run(b.q, b.cache, return_lse=True)
+    ref, ref_lse = OA.verify_attention(b.q.float().cpu().numpy(), b.cache.float().cpu().numpy(),
+                                       b.qo_indptr.cpu().numpy(), b.kv_indptr.cpu().numpy(),
+                                       b.kv_indices.cpu().numpy(), b.kv_last_page_len.cpu().numpy(),
+                                       16, mode="causal", return_lse=True)
+    check(out, ref)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=2e-2, rtol=1e-3)
+
+
+def test_tree_mask_words():
+    say("tree mask, 32 nodes")
+    b = make_verify_batch(6, 100, 2000, 32, 32, 8, 128, 16, dtype=torch.bfloat16, seed=21,
+                          tree_nodes=32).to(DEV)
+    out, _ = run_gpu(b, causal=False, tree_mask_words=b.mask_words)
+    # dense mask per request: all prefix columns + the ancestor block
+    flat = []
+    qo = np.diff(b.qo_indptr.cpu().numpy())
+    for r, L in enumerate(b.kv_lens):
+        w = b.mask_words[b.qo_indptr[r].item(): b.qo_indptr[r + 1].item()]
+        blk = ((w[:, None].astype(np.uint64) >> np.arange(qo[r], dtype=np.uint64)) & 1).astype(bool)
+        flat.append(np.concatenate([np.ones((qo[r], L - qo[r]), bool), blk], 1).ravel())
+    check(out, oracle_out(b, "custom", custom_mask=np.concatenate(flat)))
+
+
+def test_mtp_custom_mask_via_plan():
+    say("MTP (k+1)^2 custom mask through plan(custom_mask=...)")
+    k = 4
+    S = (k + 1) ** 2
+    b = make_verify_batch(4, 20, 400, S, 32, 8, 128, 16, dtype=torch.bfloat16, seed=31).to(DEV)
+    flat = M.mtp_verify_custom_mask(b.ctx.tolist(), k, device=DEV)
+    out, _ = run_gpu(b, causal=False, custom_mask=flat)
+    check(out, oracle_out(b, "custom", custom_mask=flat.cpu().numpy()))
+
+
+def test_streaming_sink_window_view():
+    say("sink+window view")
+    b = make_verify_batch(4, 3000, 9000, 1, 32, 8, 128, 16, dtype=torch.bfloat16, seed=41).to(DEV)
+    out, _ = run_gpu(b, causal=True, sink_tokens=64, window_tokens=512)
+    check(out, oracle_out(b, "streaming", sink=64, window=512))
+
+
+def test_page_permutation_invariance_bitwise():
+    say("page permutation invariance")
+    b = make_verify_batch(6, 500, 3000, 5, 32, 8, 128, 16, dtype=torch.bfloat16, seed=51,
+                          extra_pages=11).to(DEV)
+    out1, _ = run_gpu(b)
+    P = b.cache.shape[0]
+    perm = torch.randperm(P, generator=torch.Generator().manual_seed(1)).to(DEV)
+    cache2 = torch.empty_like(b.cache)
+    cache2[perm] = b.cache
+    b.cache, b.kv_indices = cache2, perm[b.kv_indices.long()].to(torch.int32)
+    out2, _ = run_gpu(b)
+    assert torch.equal(out1, out2)
+
+
+def test_tuple_cache_layout_matches_combined():
+    say("tuple (k, v) cache")
+    b = make_verify_batch(4, 100, 900, 5, 32, 8, 128, 16, dtype=torch.bfloat16, seed=61).to(DEV)
+    out1, w = run_gpu(b)
+    k, v = b.cache[:, 0].contiguous(), b.cache[:, 1].contiguous()
+    out2 = w.run(b.q, (k, v))
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+
+
+def test_graph_capture_replays():
+    say("hip graph capture of run()")
+    b = make_verify_batch(8, 200, 3000, 5, 32, 8, 128, 16, dtype=torch.bfloat16, seed=71).to(DEV)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
+    idx_buf = torch.empty(b.kv_indices.numel() + 64, dtype=torch.int32, device=DEV)
+    w = bsx.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD", use_cuda_graph=True,
+                                                paged_kv_indices_buf=idx_buf)
+    w.plan(b.qo_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, 32, 8, 128, 16,
+           causal=True, q_data_type=torch.bfloat16)
+    out = torch.empty_like(b.q)
+    eager = w.run(b.q, b.cache).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        w.run(b.q, b.cache, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        w.run(b.q, b.cache, out=out)
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+
+
+def test_config2_full_size():
+    say("config 2 full size (B=64, ctx 1k-4k, 32/8 heads, D=128)")
+    b = config2(device=DEV)
+    out, w = run_gpu(b)
+    check(out, oracle_out(b, "causal"))
+
+
+def test_config4_tree_full_size():
+    say("config 4 full size (B=32 trees of 32 nodes, ctx 2k-8k)")
+    b = config4(device=DEV)
+    out, _ = run_gpu(b, causal=False, tree_mask_words=b.mask_words)
+    qo = np.diff(b.qo_indptr.cpu().numpy())
+    flat = []
+    for r, L in enumerate(b.kv_lens):
+        w = b.mask_words[b.qo_indptr[r].item(): b.qo_indptr[r + 1].item()]
+        blk = ((w[:, None].astype(np.uint64) >> np.arange(qo[r], dtype=np.uint64)) & 1).astype(bool)
+        flat.append(np.concatenate([np.ones((qo[r], L - qo[r]), bool), blk], 1).ravel())
+    check(out, oracle_out(b, "custom", custom_mask=np.concatenate(flat)))
+
+
+def test_config3_long_context_subset():
+    say("config 3 shape, 4 requests of 32k-64k: full verify and sink+window draft")
+    b = config3(device=DEV, batch=4)
+    out, w = run_gpu(b)
+    check(out, oracle_out(b, "causal"))
+    d = make_verify_batch(4, 32768, 65536, 1, 32, 8, 128, 16, dtype=torch.bfloat16, scale=0.5,
+                          seed=1003, device=DEV)
+    out, _ = run_gpu(d, causal=True, sink_tokens=64, window_tokens=512)
+    check(out, oracle_out(d, "streaming", sink=64, window=512))
