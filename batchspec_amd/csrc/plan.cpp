@@ -50,10 +50,10 @@ struct Unit {
 }  // namespace
 
 // Resident waves per SIMD of each kernel variant (from the compiler's register
-// report: D=128 uses 164/224 VGPRs for 16/32 query rows, D=64 108/148).
+// report; 512 VGPRs per SIMD lane are shared by the resident waves).
 static int waves_per_simd(int head_dim, int qrow_tile) {
-  if (head_dim == 128) return qrow_tile == 16 ? 3 : 2;
-  return qrow_tile == 16 ? 4 : 3;
+  if (head_dim == 128) return 2;
+  return qrow_tile == 16 ? 3 : 2;
 }
 
 extern "C" int64_t bsx_attn_plan_ints_bound(int batch, int num_cus) {

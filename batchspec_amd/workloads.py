@@ -74,8 +74,8 @@ def make_verify_batch(batch: int, ctx_lo: int, ctx_hi: int, qo_len: int, num_qo_
                       num_kv_heads: int, head_dim: int, page_size: int = 16,
                       dtype: torch.dtype = torch.bfloat16, scale: float = 1.0, seed: int = 0,
                       device="cpu", tree_nodes: int = 0, extra_pages: int = 0,
-                      qo_lens: Optional[np.ndarray] = None, ctx: Optional[np.ndarray] = None
-                      ) -> VerifyBatch:
+                      qo_lens: Optional[np.ndarray] = None, ctx: Optional[np.ndarray] = None,
+                      page_order: str = "random") -> VerifyBatch:
     """Random paged batch; values drawn with a torch generator on `device`."""
     rng = np.random.default_rng(seed)
     if ctx is None:
@@ -88,6 +88,8 @@ def make_verify_batch(batch: int, ctx_lo: int, ctx_hi: int, qo_len: int, num_qo_
     kv_indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
     total_pages = int(kv_indptr[-1]) + extra_pages
     perm = rng.permutation(total_pages).astype(np.int32)[: int(kv_indptr[-1])]
+    if page_order == "sequential":
+        perm = np.arange(int(kv_indptr[-1]), dtype=np.int32)
     qo_indptr = np.concatenate([[0], np.cumsum(qo_lens)]).astype(np.int32)
     nnz = int(qo_indptr[-1])
     gen = torch.Generator(device=device).manual_seed(seed)
@@ -123,9 +125,9 @@ def config1(device="cpu", dtype=torch.float32) -> VerifyBatch:
     return make_verify_batch(4, 64, 256, 5, 8, 2, 64, 16, dtype=dtype, seed=1001, device=device)
 
 
-def config2(device="cpu", seed: int = 1002) -> VerifyBatch:
+def config2(device="cpu", seed: int = 1002, page_order: str = "random") -> VerifyBatch:
     return make_verify_batch(64, 1024, 4096, 5, 32, 8, 128, 16, dtype=torch.bfloat16, scale=0.5,
-                             seed=seed, device=device)
+                             seed=seed, device=device, page_order=page_order)
 
 
 def config3(device="cpu", seed: int = 1003, batch: int = 32) -> VerifyBatch:

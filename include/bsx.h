@@ -128,7 +128,8 @@ int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
  *   out_d      [total_qo, num_qo_heads, head_dim], same dtype as q
  *   lse_d      optional float [total_qo, num_qo_heads] log-sum-exp (natural
  *              log, of the scaled scores), or NULL
- *   float_ws_d at least plan->float_ws_bytes bytes */
+ *   float_ws_d at least plan->float_ws_bytes bytes (partial results of split
+ *              requests); runs that share one workspace must not overlap in time. */
 int bsx_attn_run(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d,
                  void* float_ws_d, int dtype, const void* q_d, int64_t q_stride_tok,
                  const void* k_cache_d, const void* v_cache_d, int64_t page_stride,
