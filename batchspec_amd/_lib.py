@@ -48,7 +48,7 @@ class AttnPlan(ctypes.Structure):
         ("num_ctas", c_int32),
         ("num_segments", c_int32),
         ("num_partials", c_int32),
-        ("num_merge_seqs", c_int32),
+        ("num_split_requests", c_int32),
         ("max_qo_len", c_int32),
         ("tile_tokens", c_int32),
         ("sink_tokens", c_int32),
@@ -62,6 +62,9 @@ class AttnPlan(ctypes.Structure):
         ("float_ws_bytes", c_int64),
         ("sm_scale", c_float),
         ("total_qo", c_int32),
+        ("safe_page_pos", c_int32),
+        ("reserved", c_int32),
+        ("total_tiles", c_int64),
     ]
 
 

@@ -40,6 +40,10 @@ namespace {
 
 constexpr int kTileTokens = 32;
 constexpr int kMaxWavesPerCta = 8;
+// Cost of starting a segment, in kv tiles: the Q load of the new request (one memory
+// latency) and the write of its (partial) result, measured on MI355X at about two
+// tile times together.
+constexpr int64_t kSegmentCost = 2;
 
 struct Unit {
   int b;
@@ -47,20 +51,56 @@ struct Unit {
   int te;
 };
 
+struct Seg {
+  int b, tb, te;
+};
+
+// Greedy packing of the units, in order, into workgroups of capacity `cap` (cost
+// units: one per tile plus kSegmentCost per segment).  Returns the number of
+// workgroups used, or -1 when more than `max_ctas` would be needed.
+int64_t pack_units(const std::vector<Unit>& units, int64_t cap, int64_t max_ctas,
+                   std::vector<std::vector<Seg>>* out) {
+  if (out) out->assign(1, {});
+  int64_t used = 1, rem = cap;
+  for (const Unit& u : units) {
+    int left = u.te - u.tb;
+    int pos = u.tb;
+    bool placed_empty = false;
+    while (left > 0 || (u.te == u.tb && !placed_empty)) {
+      if (rem < kSegmentCost + 1) {
+        if (++used > max_ctas) return -1;
+        rem = cap;
+        if (out) out->emplace_back();
+      }
+      const int take = (int)std::min<int64_t>(left, rem - kSegmentCost);
+      if (out) out->back().push_back({u.b, pos, pos + take});
+      rem -= take + kSegmentCost;
+      if (u.te == u.tb) {
+        rem -= 1;  // an empty request still writes its (zero) output
+        placed_empty = true;
+      }
+      left -= take;
+      pos += take;
+    }
+  }
+  return used;
+}
+
 }  // namespace
 
 // Resident waves per SIMD of each kernel variant (from the compiler's register
 // report; 512 VGPRs per SIMD lane are shared by the resident waves).
 static int waves_per_simd(int head_dim, int qrow_tile) {
   if (head_dim == 128) return 2;
-  return qrow_tile == 16 ? 3 : 2;
+  return qrow_tile == 16 ? 4 : 3;
 }
 
 extern "C" int64_t bsx_attn_plan_ints_bound(int batch, int num_cus) {
   if (batch < 0 || num_cus < 1) return -1;
   const int64_t num_ctas = (int64_t)num_cus * 16;
-  // seq 4B + seg_indptr (W+1) + segments 4*(W + 2B) + merge B + part_indptr (B+1)
-  return 4LL * batch + (num_ctas + 1) + 4LL * (num_ctas + 2LL * batch) + batch + (batch + 1) + 16;
+  // seq 4B + seg_indptr (W+1) + segments 4*(2W + 2B) + merge B + part_indptr (B+1)
+  return 4LL * batch + (num_ctas + 1) + 4LL * (2 * num_ctas + 2LL * batch) + batch + (batch + 1) +
+         16;
 }
 
 extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
@@ -90,6 +130,7 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   const int group = num_qo_heads / num_kv_heads;
   std::vector<int32_t> qo_len(batch), kv_len(batch);
   int max_qo = 0;
+  int safe_pos = -1;  // first position of kv_indices that belongs to a request
   for (int b = 0; b < batch; ++b) {
     const int q = qo_indptr_h[b + 1] - qo_indptr_h[b];
     const int np = kv_indptr_h[b + 1] - kv_indptr_h[b];
@@ -102,6 +143,7 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
     PLAN_REQUIRE(kl < (1LL << 30), BSX_ERR_UNSUPPORTED, "kv length too large at request %d", b);
     qo_len[b] = q;
     kv_len[b] = (int32_t)kl;
+    if (np > 0 && safe_pos < 0) safe_pos = kv_indptr_h[b];
     if (mask_mode == BSX_MASK_TREE)
       PLAN_REQUIRE(q <= 32, BSX_ERR_UNSUPPORTED,
                    "tree mask supports at most 32 query tokens per request (request %d has %d)", b,
@@ -131,8 +173,7 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   // Work units: contiguous tile ranges per request (two for the sink+window view).
   std::vector<Unit> units;
   units.reserve(2 * (size_t)batch);
-  std::vector<int> units_of(batch, 0);
-  int64_t total = 0;
+  int64_t total_tiles = 0;
   for (int b = 0; b < batch; ++b) {
     if (qo_len[b] == 0) continue;
     const int ntiles = (kv_len[b] + kTileTokens - 1) / kTileTokens;
@@ -149,37 +190,33 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
       units.push_back({b, 0, ntiles});
     }
   }
-  for (const Unit& u : units) total += std::max(1, u.te - u.tb);  // empty range still writes zeros
-
-  const int W = (int)std::max<int64_t>(1, std::min<int64_t>(num_ctas, std::max<int64_t>(total, 1)));
-
-  // Cut the virtual tile sequence into W equal shares (floor(w*T/W) boundaries).
-  struct Seg {
-    int b, tb, te;
-  };
-  std::vector<std::vector<Seg>> per_cta(W);
-  {
-    auto share_start = [&](int w) -> int64_t { return w >= W ? total : (total * w) / W; };
-    int64_t pos = 0;  // virtual position where the current unit starts
-    int w = 0;
-    for (const Unit& u : units) {
-      const int64_t cost = std::max(1, u.te - u.tb);
-      int64_t a = pos;
-      const int64_t e = pos + cost;
-      while (a < e) {
-        while (share_start(w + 1) <= a) ++w;
-        const int64_t cut = std::min(e, share_start(w + 1));
-        if (u.te == u.tb)
-          per_cta[w].push_back({u.b, u.tb, u.te});
-        else
-          per_cta[w].push_back({u.b, u.tb + (int)(a - pos), u.tb + (int)(cut - pos)});
-        a = cut;
-      }
-      pos = e;
-    }
+  int64_t total_cost = 0;
+  for (const Unit& u : units) {
+    total_tiles += u.te - u.tb;
+    total_cost += std::max(1, u.te - u.tb) + kSegmentCost;
   }
-  for (int w = 0; w < W; ++w)
-    for (const Seg& s : per_cta[w]) units_of[s.b]++;
+
+  // Smallest per-workgroup capacity whose greedy packing fits the grid.
+  std::vector<std::vector<Seg>> per_cta;
+  if (!units.empty()) {
+    const int64_t W = num_ctas;
+    int64_t lo = std::max<int64_t>(kSegmentCost + 1, (total_cost + W - 1) / W);
+    int64_t hi = total_cost + kSegmentCost + 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) / 2;
+      if (pack_units(units, mid, W, nullptr) >= 0)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    pack_units(units, lo, W, &per_cta);
+  }
+  const int W = std::max<int>(1, (int)per_cta.size());
+  if (per_cta.empty()) per_cta.resize(1);
+
+  std::vector<int> units_of(batch, 0);
+  for (const auto& v : per_cta)
+    for (const Seg& sg : v) units_of[sg.b]++;
 
   // Partial slots for requests that ended up in more than one segment.
   std::vector<int32_t> part_indptr(batch + 1, 0);
@@ -192,9 +229,9 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   std::vector<int32_t> next_slot(part_indptr.begin(), part_indptr.end() - 1);
 
   int nseg = 0;
-  for (int w = 0; w < W; ++w) nseg += (int)per_cta[w].size();
-
-  const int64_t need = 4LL * batch + (W + 1) + 4LL * nseg + (int64_t)merge_seqs.size() + (batch + 1);
+  for (const auto& v : per_cta) nseg += (int)v.size();
+  const int64_t need =
+      4LL * batch + (W + 1) + 4LL * nseg + (int64_t)merge_seqs.size() + (batch + 1);
   PLAN_REQUIRE(need <= blob_capacity_ints, BSX_ERR_CAPACITY,
                "plan blob needs %lld int32 entries, capacity %lld", (long long)need,
                (long long)blob_capacity_ints);
@@ -214,11 +251,11 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   int si = 0;
   for (int w = 0; w < W; ++w) {
     blob[off_seg_indptr + w] = si;
-    for (const Seg& s : per_cta[w]) {
-      blob[off_segments + 4 * si + 0] = s.b;
-      blob[off_segments + 4 * si + 1] = s.tb;
-      blob[off_segments + 4 * si + 2] = s.te;
-      blob[off_segments + 4 * si + 3] = units_of[s.b] > 1 ? next_slot[s.b]++ : -1;
+    for (const Seg& sg : per_cta[w]) {
+      blob[off_segments + 4 * si + 0] = sg.b;
+      blob[off_segments + 4 * si + 1] = sg.tb;
+      blob[off_segments + 4 * si + 2] = sg.te;
+      blob[off_segments + 4 * si + 3] = units_of[sg.b] > 1 ? next_slot[sg.b]++ : -1;
       ++si;
     }
   }
@@ -242,7 +279,7 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   out->num_ctas = W;
   out->num_segments = nseg;
   out->num_partials = num_partials;
-  out->num_merge_seqs = (int)merge_seqs.size();
+  out->num_split_requests = (int)merge_seqs.size();
   out->max_qo_len = max_qo;
   out->tile_tokens = kTileTokens;
   out->sink_tokens = sink_tokens;
@@ -257,5 +294,7 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   out->float_ws_bytes = (int64_t)num_partials * num_kv_heads * rows_total * (head_dim + 1) * 4;
   out->sm_scale = sm_scale > 0.f ? sm_scale : 1.0f / std::sqrt((float)head_dim);
   out->total_qo = batch > 0 ? qo_indptr_h[batch] : 0;
+  out->safe_page_pos = safe_pos;
+  out->total_tiles = total_tiles;
   return BSX_OK;
 }

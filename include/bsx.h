@@ -62,7 +62,8 @@ int bsx_version(void);
 
 /* Host-side schedule produced by bsx_attn_plan; the device half of the plan is
  * an int32 blob of `plan_ints` entries that the caller copies to device memory
- * (any stream ordering that completes before bsx_attn_run reads it). */
+ * (any stream ordering that completes before bsx_attn_run reads it); the kernels
+ * only read it, so one copied blob serves any number of runs. */
 typedef struct {
   int32_t batch;
   int32_t num_qo_heads;
@@ -76,11 +77,11 @@ typedef struct {
   int32_t heads_per_cta;  /* kv heads handled by one workgroup                */
   int32_t qblocks_per_cta;/* query-row blocks handled by one workgroup        */
   int32_t num_qgroups;    /* ceil(qrow_blocks / qblocks_per_cta)              */
-  int32_t num_ctas;       /* grid.x of the main kernel; grid.y =
+  int32_t num_ctas;       /* grid.x of the kernel; grid.y =
                              (num_kv_heads/heads_per_cta) * num_qgroups       */
   int32_t num_segments;
-  int32_t num_partials;   /* partial-result slots that need merging           */
-  int32_t num_merge_seqs; /* sequences whose kv range was split               */
+  int32_t num_partials;   /* partial-result slots of split requests           */
+  int32_t num_split_requests; /* requests whose kv range spans several segments */
   int32_t max_qo_len;
   int32_t tile_tokens;    /* kv tokens per inner-loop tile (32)               */
   int32_t sink_tokens;    /* BSX_MASK_STREAMING only                          */
@@ -94,6 +95,10 @@ typedef struct {
   int64_t float_ws_bytes; /* bytes of float workspace bsx_attn_run needs       */
   float sm_scale;
   int32_t total_qo;       /* qo_indptr[batch]                                 */
+  int32_t safe_page_pos;  /* a kv_indices position owned by some request, or -1
+                             when the page table holds no page               */
+  int32_t reserved;
+  int64_t total_tiles;    /* kv tiles of the whole schedule                   */
 } bsx_attn_plan_t;
 
 /* Size (int32 entries) of the host buffer bsx_attn_plan needs for its blob. */
@@ -128,8 +133,11 @@ int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
  *   out_d      [total_qo, num_qo_heads, head_dim], same dtype as q
  *   lse_d      optional float [total_qo, num_qo_heads] log-sum-exp (natural
  *              log, of the scaled scores), or NULL
+ *   plan_blob_d the device copy of the plan blob
  *   float_ws_d at least plan->float_ws_bytes bytes (partial results of split
- *              requests); runs that share one workspace must not overlap in time. */
+ *              requests); runs that share one workspace must not overlap in time.
+ * Two kernel launches when the plan splits requests (attention, then the merge of
+ * the partial results), one otherwise. */
 int bsx_attn_run(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d,
                  void* float_ws_d, int dtype, const void* q_d, int64_t q_stride_tok,
                  const void* k_cache_d, const void* v_cache_d, int64_t page_stride,

@@ -105,8 +105,23 @@ def test_long_context_split_and_merge():
     b = make_verify_batch(3, 20000, 40000, 5, 32, 8, 128, 16, dtype=torch.bfloat16, scale=0.5,
                           seed=11).to(DEV)
     out, w = run_gpu(b)
-    assert w.plan_info.num_merge_seqs == 3
+    assert w.plan_info.num_split_requests == 3
     check(out, oracle_out(b, "causal"))
+
+
+def test_repeated_runs_reuse_the_plan():
+    """One plan serves any number of runs; the split-and-merge path is deterministic, so
+    back-to-back runs give identical results."""
+    say("repeated runs of one plan (split requests)")
+    b = make_verify_batch(6, 3000, 9000, 5, 32, 8, 128, 16, dtype=torch.bfloat16, scale=0.5,
+                          seed=12).to(DEV)
+    out, w = run_gpu(b)
+    assert w.plan_info.num_split_requests == 6
+    check(out, oracle_out(b, "causal"))
+    for i in range(5):
+        again = w.run(b.q, b.cache)
+        torch.cuda.synchronize()
+        assert torch.equal(again, out), f"run {i}"
 
 
 def test_lse_output():
