@@ -57,8 +57,8 @@ struct Params {
   uint16_t* out;
   int64_t out_stride;
   float* lse_out;
-  float* part_o;
-  float* part_lse;
+  uint16_t* part_o;  // bf16 partial outputs (normalised), [slot][kv head][row][D]
+  float* part_lse;   // their log2-sum-exp, [slot][kv head][row]
   int num_qo_heads, num_kv_heads, group;
   int page_shift, page_mask;
   int mask_mode, sink, window;
@@ -314,8 +314,9 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
     // loads issued as soon as their registers are free.  MASKED is a compile-time
     // flag: the body loop over tiles that need no per-element mask is branch-free
     // around its loads, which keeps the compiler's load-wait counting exact.
-    auto tile_step = [&](int tile, auto masked_tag) {
+    auto tile_step = [&](int tile, auto masked_tag, auto prefetch_tag) {
       constexpr bool MASKED = decltype(masked_tag)::value;
+      constexpr bool PREFETCH = decltype(prefetch_tag)::value;
       const int j0 = tile * kTile;
       const bool last = tile + 1 >= cur.t1;
       const int pf_tile = last ? end_tile : tile + 1;
@@ -343,7 +344,7 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       // place (a load hoisted above those reads would need fresh registers and a copy
       // at the loop back-edge that waits for the load to complete).
       __builtin_amdgcn_sched_barrier(0);
-      load_tile_k(pf_tile, pf_kv, pf_pages);
+      if constexpr (PREFETCH) load_tile_k(pf_tile, pf_kv, pf_pages);
 
       if constexpr (MASKED) {
 #pragma unroll
@@ -430,7 +431,7 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
 #pragma unroll
       for (int jm = 0; jm < NJ; ++jm) asm volatile("" ::"v"(va[jm]) : "memory");
       __builtin_amdgcn_sched_barrier(0);
-      load_tile_v(pf_tile, pf_kv, pf_pages);  // V registers are free: prefetch
+      if constexpr (PREFETCH) load_tile_v(pf_tile, pf_kv, pf_pages);  // V registers are free
 #pragma unroll
       for (int jm = 0; jm < NJ; ++jm)
 #pragma unroll
@@ -445,12 +446,16 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       // [t_split, t1) touch the draft block, the kv end, or the sink/window view.
       int limit = p.mask_mode == BSX_MASK_NONE ? cur.kv_len : diag;
       if (p.mask_mode == BSX_MASK_STREAMING) limit = 0;
-      const int t_split = max(cur.t0, min(cur.t1, limit / kTile));
+      // The last tile of the workgroup's schedule has nothing to prefetch: it runs
+      // after the loops (masked form, valid for any tile).
+      const int t_end = has_next ? cur.t1 : cur.t1 - 1;
+      const int t_split = max(cur.t0, min(t_end, limit / kTile));
       for (int tile = cur.t0; tile < t_split; ++tile)
-        tile_step(tile, std::integral_constant<bool, false>());
-      for (int tile = t_split; tile < cur.t1; ++tile)
-        tile_step(tile, std::integral_constant<bool, true>());
-    } else {
+        tile_step(tile, std::false_type(), std::true_type());
+      for (int tile = t_split; tile < t_end; ++tile)
+        tile_step(tile, std::true_type(), std::true_type());
+      if (!has_next) tile_step(cur.t1 - 1, std::true_type(), std::false_type());
+    } else if (has_next) {
       // No tile ran, so the prefetched tile was not consumed: load the next
       // segment's first tile now.
       load_tile_k(end_tile, end_kv, end_pages);
@@ -473,20 +478,29 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
     }
 
     if (cur.slot >= 0) {
-      // Split request: publish this part for the merge kernel.
+      // Split request: publish this part for the merge kernel.  The normalised partial
+      // output is stored in bf16 (fp32's exponent range, so any input is safe; one
+      // extra rounding of 2^-9 relative), halving the partial traffic, which is
+      // written, flushed from L2 at kernel end and read back by the merge.  Plain
+      // stores: the pieces of a row combine into full lines in L2 (non-temporal
+      // stores measured 2.3x the write traffic).
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         if (!rowv[nt]) continue;
         const int row = row0 + nt * 16 + c16;
         const int64_t prow = ((int64_t)cur.slot * p.num_kv_heads + h) * p.qrows_total + row;
-        float* pp = p.part_o + prow * D + NJ * 4 * g4;
+        uint16_t* pp = p.part_o + prow * D + NJ * 4 * g4;
+        uint32_t packed[2 * NJ];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
-          for (int jm = 0; jm < NJ; jm += 4) {
-            f32x4 v = {o[jm][nt][e], o[jm + 1][nt][e], o[jm + 2][nt][e], o[jm + 3][nt][e]};
-            *reinterpret_cast<f32x4*>(pp + NJ * e + jm) = v;
-          }
+          for (int jm = 0; jm < NJ; jm += 2)
+            packed[(NJ * e + jm) / 2] = pack2<BSX_DTYPE_BF16>(o[jm][nt][e], o[jm + 1][nt][e]);
+#pragma unroll
+        for (int w = 0; w < 2 * NJ; w += 4) {
+          u32x4 v = {packed[w], packed[w + 1], packed[w + 2], packed[w + 3]};
+          *reinterpret_cast<u32x4*>(pp + 2 * w) = v;
+        }
         if (g4 == 0) p.part_lse[prow] = lse2[nt];
       }
     } else {
@@ -527,7 +541,7 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
 // lists are folded in with a running maximum.
 template <int DT, int D>
 __global__ void __launch_bounds__(256) merge_kernel(Params p) {
-  constexpr int TPR = D / 4;  // threads per row
+  constexpr int TPR = D / 8;  // threads per row (8 columns each)
   constexpr int RPB = 256 / TPR;
   constexpr int U = 8;        // parts loaded per round
   const int b = ld_uniform(p.blob, p.off_merge_seqs + blockIdx.x);
@@ -539,43 +553,49 @@ __global__ void __launch_bounds__(256) merge_kernel(Params p) {
   const int g = p.group;
   const int row = blockIdx.z * RPB + threadIdx.x / TPR;
   if (row >= qo_len * g) return;
-  const int d4 = (threadIdx.x % TPR) * 4;
+  const int d8 = (threadIdx.x % TPR) * 8;
   const int64_t stride = (int64_t)p.num_kv_heads * p.qrows_total;  // rows between parts
   const int64_t base0 = (int64_t)h * p.qrows_total + row;
   float mx = -INFINITY;
   float wsum = 0.f;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int q0 = pbeg; q0 < pend; q0 += U) {
     float l[U];
-    f32x4 v[U];
+    u32x4 v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int q = min(q0 + u, pend - 1);
       l[u] = q0 + u < pend ? p.part_lse[q * stride + base0] : -INFINITY;
-      v[u] = *reinterpret_cast<const f32x4*>(p.part_o + (q * stride + base0) * D + d4);
+      v[u] = *reinterpret_cast<const u32x4*>(p.part_o + (q * stride + base0) * D + d8);
     }
     float m_new = mx;
 #pragma unroll
     for (int u = 0; u < U; ++u) m_new = fmaxf(m_new, l[u]);
     if (m_new == -INFINITY) continue;  // no visible token so far
     const float alpha = __builtin_amdgcn_exp2f(mx - m_new);  // 0 when mx is -inf
-    acc *= alpha;
     wsum *= alpha;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] *= alpha;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const float w = __builtin_amdgcn_exp2f(l[u] - m_new);  // 0 for padded parts
-      acc += w * v[u];
       wsum += w;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        acc[2 * c] += w * lo_f32<BSX_DTYPE_BF16>(v[u][c]);
+        acc[2 * c + 1] += w * hi_f32<BSX_DTYPE_BF16>(v[u][c]);
+      }
     }
     mx = m_new;
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
   const int tq = row / g;
   const int hh = row - tq * g;
-  uint16_t* op = p.out + (int64_t)(qo_start + tq) * p.out_stride + (int64_t)(h * g + hh) * D + d4;
-  u32x2 pk = {pack2<DT>(acc[0] * inv, acc[1] * inv), pack2<DT>(acc[2] * inv, acc[3] * inv)};
-  *reinterpret_cast<u32x2*>(op) = pk;
-  if (p.lse_out != nullptr && d4 == 0)
+  uint16_t* op = p.out + (int64_t)(qo_start + tq) * p.out_stride + (int64_t)(h * g + hh) * D + d8;
+  u32x4 pk = {pack2<DT>(acc[0] * inv, acc[1] * inv), pack2<DT>(acc[2] * inv, acc[3] * inv),
+              pack2<DT>(acc[4] * inv, acc[5] * inv), pack2<DT>(acc[6] * inv, acc[7] * inv)};
+  *reinterpret_cast<u32x4*>(op) = pk;
+  if (p.lse_out != nullptr && d8 == 0)
     p.lse_out[(int64_t)(qo_start + tq) * p.num_qo_heads + h * g + hh] =
         (wsum > 0.f ? mx + __log2f(wsum) : -INFINITY) * 0.69314718055994531f;
 }
@@ -621,7 +641,7 @@ static int launch_all(const bsx_attn_plan_t* plan, const Params& prm, hipStream_
               : launch_main<DT, D, 2, false>(plan, prm, waves, st);
   }
   if (rc != BSX_OK || plan->num_split_requests == 0) return rc;
-  constexpr int RPB = 256 / (D / 4);
+  constexpr int RPB = 256 / (D / 8);
   const int max_rows = plan->max_qo_len * plan->group_size;
   dim3 grid(plan->num_split_requests, plan->num_kv_heads, (max_rows + RPB - 1) / RPB);
   hipLaunchKernelGGL((merge_kernel<DT, D>), grid, dim3(256), 0, st, prm);
@@ -682,12 +702,12 @@ extern "C" int bsx_attn_run(const bsx_attn_plan_t* plan, const int32_t* plan_blo
   prm.out = static_cast<uint16_t*>(out_d);
   prm.out_stride = out_stride_tok;
   prm.lse_out = lse_d;
-  // float workspace: [partial o][partial lse]
-  const int64_t part_o_floats =
+  // float workspace: [partial o (bf16)][partial lse (fp32)]
+  const int64_t part_o_elems =
       (int64_t)plan->num_partials * plan->num_kv_heads * plan->qrow_tile * plan->qrow_blocks *
       plan->head_dim;
-  prm.part_o = static_cast<float*>(float_ws_d);
-  prm.part_lse = prm.part_o ? prm.part_o + part_o_floats : nullptr;
+  prm.part_o = static_cast<uint16_t*>(float_ws_d);
+  prm.part_lse = prm.part_o ? reinterpret_cast<float*>(prm.part_o + part_o_elems) : nullptr;
   prm.num_qo_heads = plan->num_qo_heads;
   prm.num_kv_heads = plan->num_kv_heads;
   prm.group = plan->group_size;

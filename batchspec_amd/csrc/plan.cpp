@@ -291,7 +291,8 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   out->off_part_indptr = off_part;
   out->plan_ints = (int32_t)need;
   const int64_t rows_total = (int64_t)qrow_tile * qrow_blocks;
-  out->float_ws_bytes = (int64_t)num_partials * num_kv_heads * rows_total * (head_dim + 1) * 4;
+  // partial outputs in bf16 plus their fp32 log-sum-exp
+  out->float_ws_bytes = (int64_t)num_partials * num_kv_heads * rows_total * (head_dim * 2 + 4);
   out->sm_scale = sm_scale > 0.f ? sm_scale : 1.0f / std::sqrt((float)head_dim);
   out->total_qo = batch > 0 ? qo_indptr_h[batch] : 0;
   out->safe_page_pos = safe_pos;

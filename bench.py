@@ -8,19 +8,28 @@ verify attention.  A "step" is append + attention over the whole batch; three
 independent input sets rotate so the 256 MB last-level cache cannot serve repeats.
 
 Printed: one JSON line with
-  value       verify-attention HBM GB/s (algorithmic bytes / kernel time)
-  roofline    against the 8 TB/s HBM peak, from hipEvent timing of run()
+  value       verify-attention HBM GB/s: algorithmic bytes of one attention pass
+              (every K/V row of every request, Q, O and page ids once) / the mean
+              duration of BatchPrefillWithPagedKVCacheWrapper.run(), hipEvent-timed
+              on the stream the kernels run on (the pass is the attention kernel
+              plus, for split requests, the merge of their partial results)
+  roofline    the same pass against the 8 TB/s HBM peak; `traffic` is the HBM
+              bytes per pass measured with rocprofv3 counters (profiles/)
   accepted_tok_s  accepted tokens/s of a 32-layer verify step: 32 x (append +
               attention) + fused greedy acceptance over [64, 5, 128256] bf16 logits
               (draft = target argmax with probability 0.7), reference acceptance rule
   stochastic_accept  config 5 (B=128, k=5, V=128256, bf16): time and HBM fraction
   cpu_baseline    the fp32 CPU oracle on a bounded sample of the same workload
+
+`--calibrate-copy` instead times a plain 1 GiB device copy (the known-size kernel
+the HBM byte counters are scaled against).
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -30,6 +39,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "verify-attn HBM GB/s (% of 8 TB/s) + accepted tok/s, Llama-8B shape B=64 k=4"
+TRAFFIC_FILE = ROOT / "profiles" / "verify_attn_config2_traffic.txt"
 
 
 def attn_bytes(b) -> int:
@@ -51,9 +61,11 @@ def append_bytes(b) -> int:
 
 
 def time_events(fn, iters: int, warmup: int):
+    """Per-call durations (us) from hipEvents recorded on torch's current stream, which
+    is the stream every batchspec_amd entry point launches on."""
     import torch
-    for _ in range(warmup):
-        fn(0)
+    for i in range(warmup):
+        fn(i)
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
@@ -62,7 +74,7 @@ def time_events(fn, iters: int, warmup: int):
         fn(i)
         ends[i].record()
     torch.cuda.synchronize()
-    return [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]  # microseconds
+    return [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
 
 
 def median(xs):
@@ -70,9 +82,18 @@ def median(xs):
     return s[len(s) // 2]
 
 
-def cpu_baseline(sets, budget_s: float = 20.0):
-    """fp32 oracle (numpy) on a bounded sample: the first requests of the config-2 batch
-    until ~budget_s of CPU work; reported in the metric's unit (GB/s)."""
+def measured_traffic():
+    """HBM bytes per attention pass from the committed rocprofv3 counter summary."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_pass:\s*(\d+)", TRAFFIC_FILE.read_text(), re.M)
+    return int(m.group(1)) if m else None
+
+
+def cpu_baseline(sets, budget_s: float = 12.0):
+    """fp32 oracle (numpy paged gather + softmax attention) over the config-2 requests,
+    cycling through the batch until about budget_s of CPU work; reported in the
+    metric's unit (GB/s of the same algorithmic bytes)."""
     import numpy as np
     import torch
     from oracle import attention as OA
@@ -88,24 +109,42 @@ def cpu_baseline(sets, budget_s: float = 20.0):
     idx = b.kv_indices.cpu().numpy()
     last = b.kv_last_page_len.cpu().numpy()
     lens = b.kv_lens
-    t_total, done_bytes, n_req = 0.0, 0, 0
     B = len(qo) - 1
-    while t_total < budget_s and n_req < B:
-        r = n_req
+    subs = []
+    for r in range(B):
         pages = idx[kvp[r]:kvp[r + 1]]
         sub = b.cache[torch.from_numpy(pages.astype(np.int64)).to(b.cache.device)].float().cpu().numpy()
+        subs.append((pages, sub))
+    t_total, done_bytes, n_req = 0.0, 0, 0
+    while t_total < budget_s:
+        r = n_req % B
+        pages, sub = subs[r]
         t0 = time.perf_counter()
         OA.verify_attention(q[qo[r]:qo[r + 1]], sub, [0, qo[r + 1] - qo[r]],
                             [0, len(pages)], np.arange(len(pages), dtype=np.int32),
                             last[r:r + 1], b.page_size, mode="causal")
         t_total += time.perf_counter() - t0
-        done_bytes += (int(lens[r]) * b.num_kv_heads * b.head_dim * 4
-                       + 2 * (qo[r + 1] - qo[r]) * b.num_qo_heads * b.head_dim * 2 + len(pages) * 4)
+        done_bytes += (int(lens[r]) * b.num_kv_heads * b.head_dim * 2 * 2
+                       + 2 * int(qo[r + 1] - qo[r]) * b.num_qo_heads * b.head_dim * 2
+                       + len(pages) * 4)
         n_req += 1
     return {"value": round(done_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": int(cores),
             "kind": "port",
-            "sample": f"{n_req} of {B} config-2 requests, fp32 numpy paged gather + softmax "
-                      f"attention ({t_total:.1f} s)"}
+            "sample": f"{n_req} config-2 requests ({n_req / B:.1f} passes over the batch of {B}), "
+                      f"fp32 numpy paged gather + softmax attention, {t_total:.1f} s of CPU time; "
+                      "bytes counted as the bf16 algorithmic bytes of the GPU metric"}
+
+
+def calibrate_copy(reps: int = 5) -> int:
+    import torch
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    us = time_events(lambda i: dst.copy_(src), reps, 2)
+    print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n,
+                      "us": round(sum(us) / len(us), 2),
+                      "GB/s": round(2 * n / (sum(us) / len(us)) / 1e3, 1)}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -115,6 +154,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-accept", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the "
@@ -124,6 +164,9 @@ def main() -> int:
 
     import numpy as np
     import torch
+
+    if args.calibrate_copy:
+        return calibrate_copy()
 
     import batchspec_amd as bsx
     from batchspec_amd.workloads import config2, greedy_case, stochastic_case
@@ -153,7 +196,9 @@ def main() -> int:
                       b.kv_last_page_len)
         wrappers[j].run(b.q, b.cache, out=outs[j])
 
-    # --- timed steps (append + attention), whole-loop clock
+    # --- timed steps (append + attention): barrier-free single GPU, synchronize on both
+    # sides of exactly `steps` steps
+    print(f"bench: {args.warmup} warmup + {args.steps} timed steps", file=sys.stderr, flush=True)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -168,7 +213,7 @@ def main() -> int:
     ms_per_step = ev0.elapsed_time(ev1) / args.steps
     step_bytes = sum(abytes[i % 3] + pbytes[i % 3] for i in range(args.steps)) / args.steps
 
-    # --- per-launch hipEvent timing of attention run() and of the append
+    # --- per-launch hipEvent timing of the attention pass and of the append
     attn_us = time_events(lambda i: wrappers[i % 3].run(sets[i % 3].q, sets[i % 3].cache,
                                                         out=outs[i % 3]), args.steps, 3)
     app_us = time_events(lambda i: bsx.append_kv(sets[i % 3].k_new, sets[i % 3].v_new,
@@ -179,6 +224,7 @@ def main() -> int:
     t_app = sum(app_us) / len(app_us)
     a_bytes = sum(abytes) / 3
     achieved = a_bytes / (t_attn * 1e-6) / 1e9
+    p0 = wrappers[0].plan_info
     result = {
         "metric": METRIC,
         "value": round(achieved, 1),
@@ -202,11 +248,16 @@ def main() -> int:
         "attn_us": round(t_attn, 2),
         "attn_us_median": round(median(attn_us), 2),
         "append_us": round(t_app, 2),
+        "append_GBs": round(sum(pbytes) / 3 / t_app / 1e3, 1),
         "attn_bytes": int(a_bytes),
         "plan_us": round(median(plan_us), 1),
+        "plan": {"workgroups": int(p0.num_ctas), "segments": int(p0.num_segments),
+                 "split_requests": int(p0.num_split_requests), "tiles": int(p0.total_tiles)},
         "wall_s": round(wall, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
+                     "kernel": "verify attention pass (verify_attn_kernel + merge_kernel)"},
     }
 
     if not args.skip_accept:
@@ -242,6 +293,7 @@ def main() -> int:
         del s
 
     if not args.no_cpu_baseline:
+        print("bench: CPU baseline (fp32 oracle, ~12 s)", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(sets)
     print(json.dumps(result), flush=True)
     return 0
