@@ -458,152 +458,263 @@ __global__ void __launch_bounds__(256) softmax_norm_kernel(const void* logits, i
 }
 
 // ----------------------------------------------------------------------------
-// Argmax (torch semantics) in parts; partial results as (value, index).
+// Argmax (torch semantics: the first maximum wins, NaN counts as the maximum).
+//
+// One streaming pass over the flattened [rows, V] logits, cut into equal chunks of
+// elements regardless of row boundaries (every workgroup does the same work), then a
+// small combine.  A thread visits its columns in increasing order, so ties keep the
+// earlier column with a strict comparison; each 8-element vector costs one
+// NaN-propagating maximum3 reduction and a compare, and only a new maximum (rare
+// after the first few vectors) takes the branch that locates its first column.
 // ----------------------------------------------------------------------------
-__device__ __forceinline__ bool better(float av, int64_t ai, float bv, int64_t bi) {
+struct ArgmaxSplit {
+  int64_t n;      // rows * V
+  int64_t chunk;  // elements per workgroup (multiple of 8)
+  int64_t w;      // workgroups
+  int maxp;       // row pieces one workgroup can touch
+};
+
+static ArgmaxSplit argmax_split(int64_t rows, int64_t V) {
+  ArgmaxSplit a;
+  a.n = rows * V;
+  int64_t w = std::max<int64_t>(1, std::min<int64_t>(8192, ceil_div(a.n, 81920)));
+  a.chunk = ceil_div(ceil_div(a.n, w), 8) * 8;
+  a.w = ceil_div(a.n, a.chunk);
+  a.maxp = (int)(a.chunk / V) + 2;
+  return a;
+}
+
+// (av, ac) ranks before (bv, bc): NaN first (lowest column among NaNs), then the
+// larger value, then the lower column.
+__device__ __forceinline__ bool better(float av, int ac, float bv, int bc) {
   const bool an = av != av, bn = bv != bv;
-  if (an || bn) return an && (!bn || ai < bi);
-  return av > bv || (av == bv && ai < bi);
+  if (an || bn) return an && (!bn || ac < bc);
+  return av > bv || (av == bv && ac < bc);
+}
+
+__device__ __forceinline__ void take(float x, int col, float& bv, int& bc) {
+  // columns arrive in increasing order: strict rule, NaN sticks once seen
+  const bool upd = (bc == INT_MAX) || (x > bv) || ((x != x) && (bv == bv));
+  if (upd) {
+    bv = x;
+    bc = col;
+  }
 }
 
 template <int DT>
-__global__ void __launch_bounds__(256) argmax_part_kernel(const void* logits, int64_t V,
-                                                          int64_t row_stride, int64_t chunk,
-                                                          float* part_val, int64_t* part_idx) {
-  __shared__ float sv[256];
-  __shared__ int64_t si[256];
-  const int64_t r = blockIdx.x;
-  const int part = blockIdx.y;
-  const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
-  const char* row = static_cast<const char*>(logits) + r * row_stride * esz;
-  const int64_t v0 = (int64_t)part * chunk;
-  const int64_t v1 = min(V, v0 + chunk);
-  float bv = -INFINITY;
-  int64_t bi = INT64_MAX;
-  const bool vec = ((((uintptr_t)row) + v0 * esz) % 16 == 0) && (DT != BSX_DTYPE_FP32);
-  if (vec) {
-    // 8 elements per thread per step, visited in increasing index order per thread
-    for (int64_t v = v0 + 8 * threadIdx.x; v < v1; v += 8 * 256) {
-      if (v + 8 <= v1) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(row + v * esz);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float x0 = lo_f32<DT>(w[q]), x1 = hi_f32<DT>(w[q]);
-          if (better(x0, v + 2 * q, bv, bi)) { bv = x0; bi = v + 2 * q; }
-          if (better(x1, v + 2 * q + 1, bv, bi)) { bv = x1; bi = v + 2 * q + 1; }
-        }
-      } else {
-        for (int64_t u = v; u < v1; ++u) {
-          const float x = load_one<DT>(row, u);
-          if (better(x, u, bv, bi)) { bv = x; bi = u; }
-        }
-      }
-    }
+__device__ __forceinline__ void take8(const u32x4* p, int col, float& bv, int& bc) {
+  float x[8];
+  if constexpr (DT == BSX_DTYPE_FP32) {
+    const f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
+    const f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+    x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+    x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
   } else {
-    for (int64_t v = v0 + threadIdx.x; v < v1; v += 256) {
-      const float x = load_one<DT>(row, v);
-      if (better(x, v, bv, bi)) { bv = x; bi = v; }
+    const u32x4 w = *p;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      x[2 * q] = lo_f32<DT>(w[q]);
+      x[2 * q + 1] = hi_f32<DT>(w[q]);
     }
   }
-  sv[threadIdx.x] = bv;
-  si[threadIdx.x] = bi;
+  const float m = __builtin_elementwise_maximum(
+      __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[0], x[1]),
+                                    __builtin_elementwise_maximum(x[2], x[3])),
+      __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[4], x[5]),
+                                    __builtin_elementwise_maximum(x[6], x[7])));
+  const bool upd = (bc == INT_MAX) || (m > bv) || ((m != m) && (bv == bv));
+  if (upd) {
+    int e = 7;
+#pragma unroll
+    for (int q = 6; q >= 0; --q)
+      if (x[q] == m || (m != m && x[q] != x[q])) e = q;
+    bv = m;
+    bc = col + e;
+  }
+}
+
+// Reduce (bv, bc) over the 512-thread workgroup; every thread gets the result.
+constexpr int kArgmaxThreads = 512;
+__device__ __forceinline__ void block_best(float& bv, int& bc) {
+  constexpr int NW = kArgmaxThreads / 64;
+  __shared__ float s_v[NW];
+  __shared__ int s_c[NW];
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float ov = __shfl_xor(bv, m);
+    const int oc = __shfl_xor(bc, m);
+    if (better(ov, oc, bv, bc)) {
+      bv = ov;
+      bc = oc;
+    }
+  }
+  __syncthreads();  // previous readers of s_v / s_c are done
+  if ((threadIdx.x & 63) == 0) {
+    s_v[threadIdx.x >> 6] = bv;
+    s_c[threadIdx.x >> 6] = bc;
+  }
   __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) {
-      const float ov = sv[threadIdx.x + s];
-      const int64_t oi = si[threadIdx.x + s];
-      if (better(ov, oi, sv[threadIdx.x], si[threadIdx.x])) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
-      }
+  bv = s_v[0];
+  bc = s_c[0];
+#pragma unroll
+  for (int q = 1; q < NW; ++q)
+    if (better(s_v[q], s_c[q], bv, bc)) {
+      bv = s_v[q];
+      bc = s_c[q];
     }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    part_val[r * gridDim.y + part] = sv[0];
-    part_idx[r * gridDim.y + part] = si[0];
-  }
-}
-
-__device__ __forceinline__ int64_t finish_argmax(const float* pv, const int64_t* pi, int64_t r,
-                                                 int parts) {
-  float bv = pv[r * parts];
-  int64_t bi = pi[r * parts];
-  for (int q = 1; q < parts; ++q) {
-    if (better(pv[r * parts + q], pi[r * parts + q], bv, bi)) {
-      bv = pv[r * parts + q];
-      bi = pi[r * parts + q];
-    }
-  }
-  return bi;
-}
-
-__global__ void argmax_final_kernel(const float* pv, const int64_t* pi, int64_t rows, int parts,
-                                    int64_t* out) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r < rows) out[r] = finish_argmax(pv, pi, r, parts);
-}
-
-__global__ void greedy_eval_kernel(const int64_t* draft, const int64_t* target_ids,
-                                   const float* pv, const int64_t* pi, int parts, int B, int k,
-                                   int64_t eos, int mode, int64_t* bonus, int64_t* accept,
-                                   uint8_t* eos_acc) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= B) return;
-  int64_t pred[64 + 1];
-  for (int i = 0; i <= k; ++i) {
-    const int64_t r = (int64_t)b * (k + 1) + i;
-    pred[i] = target_ids ? target_ids[r] : finish_argmax(pv, pi, r, parts);
-  }
-  int64_t n = 0;
-  bool prefix = true;
-  bool eos_hit = false;
-  for (int i = 0; i < k; ++i) {
-    const int64_t d = draft[(int64_t)b * k + i];
-    const bool f = pred[i] == d;
-    if (mode == 0) {
-      n += f ? 1 : 0;
-    } else {
-      prefix = prefix && f;
-      n += prefix ? 1 : 0;
-    }
-    const bool counted = mode == 0 ? f : (prefix && f);
-    eos_hit = eos_hit || (counted && d == eos);
-  }
-  accept[b] = n + 1;
-  bonus[b] = pred[n];
-  eos_acc[b] = eos_hit ? 1 : 0;
-}
-
-static int argmax_parts(int64_t rows, int64_t V) {
-  int64_t p = ceil_div(2048, std::max<int64_t>(rows, 1));
-  p = std::min<int64_t>(p, ceil_div(V, 2048));
-  return (int)std::max<int64_t>(1, std::min<int64_t>(p, 64));
 }
 
 template <int DT>
-static int launch_argmax_parts(const void* logits, int64_t rows, int64_t V, int64_t stride,
-                               int parts, float* pv, int64_t* pi, hipStream_t st) {
-  const int64_t chunk = ceil_div(ceil_div(V, parts), 8) * 8;
-  hipLaunchKernelGGL((argmax_part_kernel<DT>), dim3((unsigned)rows, parts), dim3(256), 0, st,
-                     logits, V, stride, chunk, pv, pi);
-  BSX_LAUNCH_CHECK();
-  return BSX_OK;
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_split_kernel(const void* logits, int64_t V,
+                                                           int64_t row_stride, int64_t n,
+                                                           int64_t chunk, int maxp, float* pval,
+                                                           int32_t* pcol) {
+  constexpr int ES = DT == BSX_DTYPE_FP32 ? 4 : 2;
+  const int64_t e0 = (int64_t)blockIdx.x * chunk;
+  const int64_t e1 = min(n, e0 + chunk);
+  const int t = threadIdx.x;
+  int piece = 0;
+  for (int64_t s = e0; s < e1; ++piece) {
+    const int64_t r = s / V;
+    const int64_t c0 = s - r * V;
+    const int64_t c1 = min(V, c0 + (e1 - s));
+    const char* row = static_cast<const char*>(logits) + r * row_stride * ES;
+    float bv = -INFINITY;
+    int bc = INT_MAX;
+    // head (unaligned), body (8-element vectors), tail: each thread's columns ascend
+    int64_t a0 = c0, a1 = c0;
+    if ((((uintptr_t)row) % 16) == 0) {
+      a0 = min(c1, (c0 + 7) / 8 * 8);
+      a1 = max(a0, c1 / 8 * 8);
+    }
+    constexpr int NT = kArgmaxThreads;
+    if (c0 + t < a0) take(load_one<DT>(row, c0 + t), (int)(c0 + t), bv, bc);
+    const int64_t nv = (a1 - a0) / 8;
+    const u32x4* vbase = reinterpret_cast<const u32x4*>(row + a0 * ES);
+    // the logits are read once: non-temporal loads, 8 vectors in flight per thread
+    constexpr int U = 8 / (ES / 2);
+    int64_t v = t;
+    for (; v + (U - 1) * NT < nv; v += U * NT) {
+      u32x4 buf[U][ES / 2];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int h = 0; h < ES / 2; ++h)
+          buf[u][h] = __builtin_nontemporal_load(vbase + (v + u * NT) * (ES / 2) + h);
+#pragma unroll
+      for (int u = 0; u < U; ++u) take8<DT>(buf[u], (int)(a0 + 8 * (v + u * NT)), bv, bc);
+    }
+    for (; v < nv; v += NT) take8<DT>(vbase + v * (ES / 2), (int)(a0 + 8 * v), bv, bc);
+    for (int64_t c = a1 + t; c < c1; c += NT) take(load_one<DT>(row, c), (int)c, bv, bc);
+    block_best(bv, bc);
+    if (t == 0) {
+      pval[(int64_t)blockIdx.x * maxp + piece] = bv;
+      pcol[(int64_t)blockIdx.x * maxp + piece] = bc;
+    }
+    s += c1 - c0;
+  }
 }
 
-static int dispatch_argmax_parts(const void* logits, int dtype, int64_t rows, int64_t V,
-                                 int64_t stride, int parts, float* pv, int64_t* pi,
+// argmax of row r from the partials of the workgroups whose chunks cover it (the
+// first four loaded together, any further ones after).
+__device__ __forceinline__ int64_t row_argmax(const float* pval, const int32_t* pcol, int64_t r,
+                                              int64_t V, int64_t chunk, int maxp) {
+  const int64_t w0 = (r * V) / chunk;
+  const int64_t w1 = ((r + 1) * V - 1) / chunk;
+  float v[4];
+  int c[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t w = min(w0 + q, w1);
+    const int64_t piece = r - (w * chunk) / V;
+    v[q] = pval[w * maxp + piece];
+    c[q] = pcol[w * maxp + piece];
+  }
+  float bv = v[0];
+  int bc = c[0];
+#pragma unroll
+  for (int q = 1; q < 4; ++q)
+    if (better(v[q], c[q], bv, bc)) {
+      bv = v[q];
+      bc = c[q];
+    }
+  for (int64_t w = w0 + 4; w <= w1; ++w) {
+    const int64_t piece = r - (w * chunk) / V;
+    const float x = pval[w * maxp + piece];
+    const int cx = pcol[w * maxp + piece];
+    if (better(x, cx, bv, bc)) {
+      bv = x;
+      bc = cx;
+    }
+  }
+  return bc;
+}
+
+__global__ void argmax_final_kernel(const float* pval, const int32_t* pcol, int64_t rows, int64_t V,
+                                    int64_t chunk, int maxp, int64_t* out) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r < rows) out[r] = row_argmax(pval, pcol, r, V, chunk, maxp);
+}
+
+// One wave per request: lane i < k+1 owns row (b, i); the evaluation of
+// mtp_engine.py:553-560 runs on ballots and shuffles.
+__global__ void __launch_bounds__(256) greedy_eval_kernel(
+    const int64_t* draft, const int64_t* target_ids, const float* pval, const int32_t* pcol,
+    int64_t V, int64_t chunk, int maxp, int B, int k, int64_t eos, int mode, int64_t* bonus,
+    int64_t* accept, uint8_t* eos_acc) {
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= B) return;
+  const int i = threadIdx.x & 63;
+  int64_t pred = -1;
+  if (i <= k) {
+    const int64_t r = (int64_t)b * (k + 1) + i;
+    pred = target_ids ? target_ids[r] : row_argmax(pval, pcol, r, V, chunk, maxp);
+  }
+  const int64_t d = i < k ? draft[(int64_t)b * k + i] : -2;
+  const bool flag = i < k && pred == d;
+  const uint64_t fl = __builtin_amdgcn_ballot_w64(flag);
+  uint64_t counted;
+  if (mode == 0) {
+    counted = fl;
+  } else {
+    // longest matching prefix: the run of ones from bit 0
+    const uint64_t miss = ~fl;
+    const int first_miss = miss ? __builtin_ctzll(miss) : 64;
+    counted = first_miss >= 64 ? fl : (fl & ((1ull << first_miss) - 1));
+  }
+  const int n = __builtin_popcountll(counted);
+  const bool my_counted = (counted >> i) & 1ull;
+  const uint64_t eh = __builtin_amdgcn_ballot_w64(my_counted && d == eos);
+  const int64_t bonus_v = __shfl(pred, n);
+  if (i == 0) {
+    accept[b] = n + 1;
+    bonus[b] = bonus_v;
+    eos_acc[b] = eh ? 1 : 0;
+  }
+}
+
+static int dispatch_argmax_split(const void* logits, int dtype, int64_t rows, int64_t V,
+                                 int64_t stride, const ArgmaxSplit& sp, float* pv, int32_t* pc,
                                  hipStream_t st) {
   switch (dtype) {
     case BSX_DTYPE_BF16:
-      return launch_argmax_parts<BSX_DTYPE_BF16>(logits, rows, V, stride, parts, pv, pi, st);
+      hipLaunchKernelGGL((argmax_split_kernel<BSX_DTYPE_BF16>), dim3((unsigned)sp.w), dim3(kArgmaxThreads), 0,
+                         st, logits, V, stride, sp.n, sp.chunk, sp.maxp, pv, pc);
+      break;
     case BSX_DTYPE_FP16:
-      return launch_argmax_parts<BSX_DTYPE_FP16>(logits, rows, V, stride, parts, pv, pi, st);
+      hipLaunchKernelGGL((argmax_split_kernel<BSX_DTYPE_FP16>), dim3((unsigned)sp.w), dim3(kArgmaxThreads), 0,
+                         st, logits, V, stride, sp.n, sp.chunk, sp.maxp, pv, pc);
+      break;
     case BSX_DTYPE_FP32:
-      return launch_argmax_parts<BSX_DTYPE_FP32>(logits, rows, V, stride, parts, pv, pi, st);
+      hipLaunchKernelGGL((argmax_split_kernel<BSX_DTYPE_FP32>), dim3((unsigned)sp.w), dim3(kArgmaxThreads), 0,
+                         st, logits, V, stride, sp.n, sp.chunk, sp.maxp, pv, pc);
+      break;
+    default:
+      set_error("unknown dtype %d", dtype);
+      return BSX_ERR_INVALID;
   }
-  set_error("unknown dtype %d", dtype);
-  return BSX_ERR_INVALID;
+  BSX_LAUNCH_CHECK();
+  return BSX_OK;
 }
 
 static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -614,27 +725,29 @@ static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 using namespace bsx;
 
 extern "C" int64_t bsx_argmax_ws_bytes(int64_t rows, int64_t vocab) {
-  const int parts = acc::argmax_parts(rows, vocab);
-  return acc::align256(rows * parts * 4) + rows * parts * 8;
+  if (rows <= 0 || vocab <= 0) return 256;
+  const acc::ArgmaxSplit sp = acc::argmax_split(rows, vocab);
+  return acc::align256(sp.w * sp.maxp * 4) + sp.w * sp.maxp * 4;
 }
 
 extern "C" int bsx_argmax(const void* logits_d, int dtype, int64_t rows, int64_t vocab,
                           int64_t row_stride, int64_t* out_d, void* ws_d, int64_t ws_bytes,
                           void* stream) {
-  BSX_REQUIRE(rows >= 0 && vocab > 0, BSX_ERR_INVALID, "bad shape rows=%lld vocab=%lld",
-              (long long)rows, (long long)vocab);
+  BSX_REQUIRE(rows >= 0 && vocab > 0 && vocab < (1LL << 31), BSX_ERR_INVALID,
+              "bad shape rows=%lld vocab=%lld", (long long)rows, (long long)vocab);
   if (rows == 0) return BSX_OK;
   BSX_REQUIRE(logits_d && out_d && ws_d, BSX_ERR_INVALID, "null pointer");
+  BSX_REQUIRE(row_stride >= vocab, BSX_ERR_INVALID, "row_stride smaller than vocab");
   BSX_REQUIRE(ws_bytes >= bsx_argmax_ws_bytes(rows, vocab), BSX_ERR_CAPACITY,
               "argmax workspace too small");
-  const int parts = acc::argmax_parts(rows, vocab);
+  const acc::ArgmaxSplit sp = acc::argmax_split(rows, vocab);
   float* pv = static_cast<float*>(ws_d);
-  int64_t* pi = reinterpret_cast<int64_t*>(static_cast<char*>(ws_d) + acc::align256(rows * parts * 4));
+  int32_t* pc = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) + acc::align256(sp.w * sp.maxp * 4));
   hipStream_t st = as_stream(stream);
-  int rc = acc::dispatch_argmax_parts(logits_d, dtype, rows, vocab, row_stride, parts, pv, pi, st);
+  int rc = acc::dispatch_argmax_split(logits_d, dtype, rows, vocab, row_stride, sp, pv, pc, st);
   if (rc != BSX_OK) return rc;
   hipLaunchKernelGGL(acc::argmax_final_kernel, dim3((unsigned)ceil_div(rows, 256)), dim3(256), 0,
-                     st, pv, pi, rows, parts, out_d);
+                     st, pv, pc, rows, vocab, sp.chunk, sp.maxp, out_d);
   BSX_LAUNCH_CHECK();
   return BSX_OK;
 }
@@ -648,7 +761,7 @@ extern "C" int bsx_accept_greedy(const int64_t* draft_d, const int64_t* target_i
                                  int64_t vocab, int64_t eos_id, int mode, int64_t* bonus_d,
                                  int64_t* accept_d, uint8_t* eos_acc_d, void* ws_d,
                                  int64_t ws_bytes, void* stream) {
-  BSX_REQUIRE(B >= 0 && k >= 0 && k <= 64, BSX_ERR_INVALID, "bad B=%d / k=%d (k <= 64)", B, k);
+  BSX_REQUIRE(B >= 0 && k >= 0 && k <= 63, BSX_ERR_INVALID, "bad B=%d / k=%d (k <= 63)", B, k);
   BSX_REQUIRE(mode == 0 || mode == 1, BSX_ERR_INVALID, "mode must be 0 or 1");
   if (B == 0) return BSX_OK;
   BSX_REQUIRE(bonus_d && accept_d && eos_acc_d && (k == 0 || draft_d), BSX_ERR_INVALID,
@@ -657,21 +770,21 @@ extern "C" int bsx_accept_greedy(const int64_t* draft_d, const int64_t* target_i
   hipStream_t st = as_stream(stream);
   const int64_t rows = (int64_t)B * (k + 1);
   float* pv = nullptr;
-  int64_t* pi = nullptr;
-  int parts = 1;
+  int32_t* pc = nullptr;
+  acc::ArgmaxSplit sp = {0, 1, 0, 1};
   if (!target_ids_d) {
-    BSX_REQUIRE(vocab > 0, BSX_ERR_INVALID, "vocab must be > 0");
+    BSX_REQUIRE(vocab > 0 && vocab < (1LL << 31), BSX_ERR_INVALID, "vocab must be in (0, 2^31)");
     BSX_REQUIRE(ws_d && ws_bytes >= bsx_accept_greedy_ws_bytes(B, k, vocab), BSX_ERR_CAPACITY,
                 "greedy workspace too small");
-    parts = acc::argmax_parts(rows, vocab);
+    sp = acc::argmax_split(rows, vocab);
     pv = static_cast<float*>(ws_d);
-    pi = reinterpret_cast<int64_t*>(static_cast<char*>(ws_d) + acc::align256(rows * parts * 4));
-    int rc = acc::dispatch_argmax_parts(target_logits_d, dtype, rows, vocab, vocab, parts, pv, pi, st);
+    pc = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) + acc::align256(sp.w * sp.maxp * 4));
+    int rc = acc::dispatch_argmax_split(target_logits_d, dtype, rows, vocab, vocab, sp, pv, pc, st);
     if (rc != BSX_OK) return rc;
   }
-  hipLaunchKernelGGL(acc::greedy_eval_kernel, dim3((unsigned)ceil_div(B, 64)), dim3(64), 0, st,
-                     draft_d, target_ids_d, pv, pi, parts, B, k, eos_id, mode, bonus_d, accept_d,
-                     eos_acc_d);
+  hipLaunchKernelGGL(acc::greedy_eval_kernel, dim3((unsigned)ceil_div(B, 4)), dim3(256), 0, st,
+                     draft_d, target_ids_d, pv, pc, vocab, sp.chunk, sp.maxp, B, k, eos_id, mode,
+                     bonus_d, accept_d, eos_acc_d);
   BSX_LAUNCH_CHECK();
   return BSX_OK;
 }

@@ -76,7 +76,8 @@ def _greedy(draft: torch.Tensor, preds: torch.Tensor, eos: int, mode: int):
     else:
         raise ValueError("target_preds must be ids [B, k+1] or logits [B, k+1, V]")
     _lib.check(rc, "evaluate_posterior")
-    return bonus[:, None], accept, eos_acc.bool()[:, None]
+    # the kernel writes 0/1 bytes: a bool view, no conversion kernel
+    return bonus[:, None], accept, eos_acc.view(torch.bool)[:, None]
 
 
 class PosteriorMixin:
