@@ -86,6 +86,8 @@ SIGNATURES = {
                                           _P, _P, c_int, c_int, c_int, c_int, _P]),
     "bsx_kv_append": (c_int, [_P, _P, c_int64, c_int64, _P, _P, _P, _P, c_int, c_int, _P, _P,
                               c_int64, c_int, c_int, c_int, c_int, _P]),
+    "bsx_collate_accepted_kv": (c_int, [_P, _P, c_int, c_int, _P, _P, _P, _P, c_int, c_int64,
+                                        c_int, c_int, c_int, c_int, _P]),
     "bsx_argmax_ws_bytes": (c_int64, [c_int64, c_int64]),
     "bsx_argmax": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, _P]),
     "bsx_accept_greedy_ws_bytes": (c_int64, [c_int, c_int, c_int64]),

@@ -36,6 +36,7 @@ HIP_COMMON = [
 HIP_SOURCES = {
     "attn.hip": [],
     "append.hip": [],
+    "collate.hip": [],
     "accept.hip": ["-ffp-contract=off"],
 }
 CXX_SOURCES = ["abi.cpp", "plan.cpp"]

@@ -279,6 +279,19 @@ def main() -> int:
         result["greedy_accept"] = {"us": round(t_acc, 2), "GB/s": round(gbytes / t_acc / 1e3, 1),
                                    "frac": round(gbytes / t_acc / 1e3 / HBM_PEAK_GBS, 4)}
         result["verify_step_32_layers_us"] = round(t_model, 1)
+        # accepted-KV compaction (collate_accepted_kv_cache) of the same accept counts over
+        # the three config-2 caches taken as three layers: rows prev + i*(k+1) -> prev + i
+        from batchspec_amd.collate import collate_accepted_kv_cache
+        kvl = torch.from_numpy(np.ascontiguousarray(sets[0].kv_lens)).to(dev)
+        prev = (kvl - 25).to(torch.int32)
+        caches = [b.cache for b in sets]
+        col_us = time_events(lambda i: collate_accepted_kv_cache(
+            acc_ref, prev, 4, caches, sets[0].kv_indptr, sets[0].kv_indices), args.steps, 3)
+        t_col = sum(col_us) / len(col_us)
+        moved = int((acc_ref.clamp(max=5) - 1).clamp(min=0).sum()) * 2 * 8 * 128 * 2 * 2 * 3
+        result["collate_accepted_kv"] = {"us_3_layers": round(t_col, 2),
+                                         "bytes_moved": moved,
+                                         "GB/s": round(moved / t_col / 1e3, 1)}
         del gl, g
         # stochastic acceptance (config 5)
         s = stochastic_case(device=dev)

@@ -182,6 +182,23 @@ int bsx_kv_append(const void* k_d, const void* v_d, int64_t k_stride_tok,
                   void* v_cache_d, int64_t page_stride, int num_kv_heads, int head_dim,
                   int page_size, int elem_bytes, void* stream);
 
+/* MTPEngine.collate_accepted_kv_cache (batchspec/backends/mtp_engine.py:577-631)
+ * without the per-layer whole-cache copy: for every layer and request b the KV rows
+ * of the accepted regular tokens, at positions prev_cachelens[b] + i*(draft_length+1)
+ * for 1 <= i < accept_nums[b], move in place to positions prev_cachelens[b] + i,
+ * addressed through the page table (no contiguous-page assumption).  The page-table
+ * trim that follows (delete_kv, mtp_engine.py:630-631) stays on the host.
+ *   accept_nums_d [B] int64 (clamped to [0, draft_length+1]); prev_cachelens_d [B]
+ *   int32; k_bases_d / v_bases_d: device arrays of num_layers 16-byte aligned base
+ *   addresses of each layer's K and V views (same page stride and shape for all
+ *   layers).  Positions beyond a request's pages are skipped. */
+int bsx_collate_accepted_kv(const int64_t* accept_nums_d, const int32_t* prev_cachelens_d,
+                            int batch, int draft_length, const int32_t* kv_indptr_d,
+                            const int32_t* kv_indices_d, const int64_t* k_bases_d,
+                            const int64_t* v_bases_d, int num_layers, int64_t page_stride,
+                            int num_kv_heads, int head_dim, int page_size, int elem_bytes,
+                            void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* 3. Acceptance                                                              */
 /* ------------------------------------------------------------------------- */
