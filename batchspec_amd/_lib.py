@@ -63,7 +63,7 @@ class AttnPlan(ctypes.Structure):
         ("sm_scale", c_float),
         ("total_qo", c_int32),
         ("safe_page_pos", c_int32),
-        ("reserved", c_int32),
+        ("shared_kv_tiles", c_int32),
         ("total_tiles", c_int64),
     ]
 

@@ -34,12 +34,13 @@
 //     cost more than the separate launch.)
 #include <type_traits>
 
+#include "attn_shape.h"
 #include "common.h"
 
 namespace bsx {
 namespace attn {
 
-constexpr int kTile = 32;
+constexpr int kTile = attn_shape::kTileTokens;
 // Raise the softmax reference maximum only past this margin (log2 units).
 constexpr float kRescaleMargin = 8.0f;
 
@@ -125,9 +126,23 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
   }
 }
 
+// Two fp32 values to packed 16-bit (round to nearest even): one v_cvt_pk_* each.
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)f32_to_half_bits<DT>(lo) | ((uint32_t)f32_to_half_bits<DT>(hi) << 16);
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  if constexpr (DT == BSX_DTYPE_BF16) {
+    typedef __bf16 h2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, h2_t));
+  } else {
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, h2_t));
+  }
+}
+
+// NaN-propagating maximum (v_maximum3_f32): unlike fmaxf it needs no quieting of
+// its inputs.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
 // Per-row visibility rule of the masked tiles, in a form that is the same for every
@@ -142,6 +157,218 @@ struct RowMask {
   int lim;
   uint32_t word;
 };
+
+// Applies the RowMask rule to the transposed scores of one tile: lane (c16, g4) holds
+// query row c16 of tile nt against kv tokens j0 + 16 st + 4 g4 + e.
+template <int NT>
+__device__ __forceinline__ void mask_tile(f32x4 (&sacc)[2][NT], const RowMask (&rm)[NT], int j0,
+                                          int g4, int diag, int sink_end, int win_beg) {
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = j0 + 16 * st + 4 * g4 + e;
+      const int d = j - diag;
+      const bool in_view = (j < sink_end) | (j >= win_beg);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t bit = (rm[nt].word >> (uint32_t)min(max(d, 0), 31)) & 1u;
+        const bool vis = (j <= rm[nt].lim) & ((d < 0) | (bit != 0u)) & in_view;
+        sacc[st][nt][e] = vis ? sacc[st][nt][e] : -INFINITY;
+      }
+    }
+}
+
+// Online softmax of one tile against the reference maximum m_ref (exp2 domain, scores
+// scaled by scale_log2).  The reference is raised, and O and l rescaled, only when some
+// row's scaled maximum exceeds it by more than the margin (always on the first visible
+// tile).  Returns the probabilities packed as the B operand of O^T += V^T P^T.
+template <int DT, int NJ, int NT>
+__device__ __forceinline__ void softmax_tile(const f32x4 (&sacc)[2][NT], float scale_log2,
+                                             float (&m_ref)[NT], float (&l_run)[NT],
+                                             f32x4 (&o)[NJ][NT], uint32_t (&pb)[NT][4]) {
+  bool need = false;
+  float tmax[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const float mx = max3f(max3f(sacc[0][nt][0], sacc[0][nt][1], sacc[0][nt][2]),
+                           max3f(sacc[0][nt][3], sacc[1][nt][0], sacc[1][nt][1]),
+                           __builtin_elementwise_maximum(sacc[1][nt][2], sacc[1][nt][3]));
+    tmax[nt] = mx * scale_log2;
+    need |= tmax[nt] > m_ref[nt] + kRescaleMargin;
+  }
+  if (__builtin_amdgcn_ballot_w64(need) != 0) {
+    // wave-uniform and rare: row maxima over the 4 lane groups, then rescale
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      float mx = tmax[nt];
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_ref[nt], mx);
+      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref[nt] - m_new);
+      l_run[nt] *= alpha;
+#pragma unroll
+      for (int jm = 0; jm < NJ; ++jm) o[jm][nt] *= alpha;
+      m_ref[nt] = m_new;
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const float neg_m = m_ref[nt] == -INFINITY ? 0.f : -m_ref[nt];
+    float pv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[e >> 2][nt][e & 3], scale_log2, neg_m));
+      l_run[nt] += pv[e];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pb[nt][r] = pack2<DT>(pv[2 * r], pv[2 * r + 1]);
+  }
+}
+
+// V rows of tokens at or past kv_len hold unrelated data: zero them (their
+// probabilities are 0, but 0 * Inf/NaN would not be).
+template <int VW>
+__device__ __forceinline__ void zero_rows_past_end(uint32_t (&vraw)[8][VW], int j0, int g4,
+                                                   int kv_len) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const bool ok = j0 + 16 * (e >> 2) + 4 * g4 + (e & 3) < kv_len;
+#pragma unroll
+    for (int w = 0; w < VW; ++w) vraw[e][w] = ok ? vraw[e][w] : 0u;
+  }
+}
+
+// V^T operands from 8 token rows per lane: A_jm[e] = V[tau(g4, e)][NJ*c16 + jm]
+// (8x8 transpose of 16-bit values with v_perm_b32).
+template <int NJ, int VW>
+__device__ __forceinline__ void transpose_v(const uint32_t (&vraw)[8][VW], u32x4 (&va)[NJ]) {
+#pragma unroll
+  for (int jm = 0; jm < NJ; ++jm) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t w0 = vraw[2 * r][jm >> 1];
+      const uint32_t w1 = vraw[2 * r + 1][jm >> 1];
+      va[jm][r] = (jm & 1) ? perm_hi(w0, w1) : perm_lo(w0, w1);
+    }
+  }
+}
+
+template <int DT, int NJ, int NT>
+__device__ __forceinline__ void pv_tile(const u32x4 (&va)[NJ], const uint32_t (&pb)[NT][4],
+                                        f32x4 (&o)[NJ][NT]) {
+#pragma unroll
+  for (int jm = 0; jm < NJ; ++jm)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      u32x4 bop = {pb[nt][0], pb[nt][1], pb[nt][2], pb[nt][3]};
+      o[jm][nt] = mfma16x16x32<DT>(va[jm], bop, o[jm][nt]);
+    }
+}
+
+// End of a segment: normalise and store the wave's rows as the request's output, or,
+// for a split request, as a bf16 partial with its log2-sum-exp for the merge kernel.
+// Lane (c16, g4) holds row c16 of tile nt at d = NJ*(4 g4 + e) + jm (INTERLEAVED,
+// 4 NJ consecutive values per lane) or at d = 16 jm + 4 g4 + e (runs of 4).
+template <int DT, int D, int NT, bool INTERLEAVED>
+__device__ __forceinline__ void store_row(uint16_t* dst, int g4, const f32x4 (&o)[D / 16][NT],
+                                          int nt) {
+  constexpr int NJ = D / 16;
+  if constexpr (INTERLEAVED) {
+    uint32_t packed[2 * NJ];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int jm = 0; jm < NJ; jm += 2)
+        packed[(NJ * e + jm) / 2] = pack2<DT>(o[jm][nt][e], o[jm + 1][nt][e]);
+    uint16_t* d0 = dst + NJ * 4 * g4;
+#pragma unroll
+    for (int w = 0; w < 2 * NJ; w += 4) {
+      u32x4 v = {packed[w], packed[w + 1], packed[w + 2], packed[w + 3]};
+      *reinterpret_cast<u32x4*>(d0 + 2 * w) = v;
+    }
+  } else {
+#pragma unroll
+    for (int jm = 0; jm < NJ; ++jm) {
+      u32x2 v = {pack2<DT>(o[jm][nt][0], o[jm][nt][1]), pack2<DT>(o[jm][nt][2], o[jm][nt][3])};
+      *reinterpret_cast<u32x2*>(dst + 16 * jm + 4 * g4) = v;
+    }
+  }
+}
+
+template <int DT, int D, int NT, bool INTERLEAVED = true>
+__device__ __forceinline__ void finish_segment(const Params& p, const Seg& cur, int h, int row0,
+                                               int c16, int g4, f32x4 (&o)[D / 16][NT],
+                                               const float (&m_ref)[NT],
+                                               const float (&l_run)[NT]) {
+  constexpr int NJ = D / 16;
+  const int g = p.group;
+  const int nrows = cur.qo_len * g;
+  float lse2[NT];
+  bool rowv[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float l = l_run[nt];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int jm = 0; jm < NJ; ++jm) o[jm][nt] *= inv;
+    lse2[nt] = l > 0.f ? m_ref[nt] + __log2f(l) : -INFINITY;
+    rowv[nt] = row0 + nt * 16 + c16 < nrows;
+  }
+
+  if (cur.slot >= 0) {
+    // Split request: publish this part for the merge kernel.  The normalised partial
+    // output is stored in bf16 (fp32's exponent range, so any input is safe; one
+    // extra rounding of 2^-9 relative), halving the partial traffic, which is
+    // written, flushed from L2 at kernel end and read back by the merge.  Plain
+    // stores: the pieces of a row combine into full lines in L2 (non-temporal
+    // stores measured 2.3x the write traffic).
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (!rowv[nt]) continue;
+      const int row = row0 + nt * 16 + c16;
+      const int64_t prow = ((int64_t)cur.slot * p.num_kv_heads + h) * p.qrows_total + row;
+      store_row<BSX_DTYPE_BF16, D, NT, INTERLEAVED>(p.part_o + prow * D, g4, o, nt);
+      if (g4 == 0) p.part_lse[prow] = lse2[nt];
+    }
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (!rowv[nt]) continue;
+      const int row = row0 + nt * 16 + c16;
+      const int tq = row / g;
+      const int hh = row - tq * g;
+      uint16_t* op =
+          p.out + (int64_t)(cur.qo_start + tq) * p.out_stride + (int64_t)(h * g + hh) * D;
+      store_row<DT, D, NT, INTERLEAVED>(op, g4, o, nt);
+      if (p.lse_out != nullptr && g4 == 0)
+        p.lse_out[(int64_t)(cur.qo_start + tq) * p.num_qo_heads + h * g + hh] =
+            lse2[nt] * 0.69314718055994531f;
+    }
+  }
+}
+
+// Row masks of the wave's query rows for request `cur` (padded rows take the last
+// query token's rule; their results are never stored).
+template <int NT>
+__device__ __forceinline__ void row_masks(const Params& p, const Seg& cur, int row0, int c16,
+                                          RowMask (&rm)[NT]) {
+  const bool causal_like = p.mask_mode == BSX_MASK_CAUSAL || p.mask_mode == BSX_MASK_STREAMING;
+  const int nrows = cur.qo_len * p.group;
+  const int diag = cur.kv_len - cur.qo_len;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = row0 + nt * 16 + c16;
+    const bool rv = row < nrows;
+    const int tq = rv ? row / p.group : 0;
+    const int tq_m = rv ? tq : cur.qo_len - 1;
+    rm[nt].lim = causal_like ? diag + tq_m : cur.kv_len - 1;
+    rm[nt].word = ~0u;
+    if (p.mask_mode == BSX_MASK_TREE && rv) rm[nt].word = p.mask_words[cur.qo_start + tq];
+  }
+}
 
 // NT: query-row tiles of 16 per wave.  D: head dim (64 or 128).
 template <int DT, int D, int NT, bool PS_GE16>
@@ -268,21 +495,16 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
 
     // ---- Q (B operand of S^T = K Q^T): lane holds query row c16 of tile nt, d chunk
     // (s, g4).  Padded rows read row 0 (finite data; their results are never stored).
-    const bool causal_like = p.mask_mode == BSX_MASK_CAUSAL || p.mask_mode == BSX_MASK_STREAMING;
     const int sink_end = p.mask_mode == BSX_MASK_STREAMING ? p.sink : cur.kv_len;
     const int win_beg = p.mask_mode == BSX_MASK_STREAMING ? cur.kv_len - p.window : cur.kv_len;
     RowMask rm[NT];
+    row_masks<NT>(p, cur, row0, c16, rm);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int row = row0 + nt * 16 + c16;
       const bool rv = row < nrows;
       const int tq = rv ? row / g : 0;
       const int hh = rv ? row - tq * g : 0;
-      // padded rows take the last query token's rule (their results are never stored)
-      const int tq_m = rv ? tq : cur.qo_len - 1;
-      rm[nt].lim = causal_like ? diag + tq_m : cur.kv_len - 1;
-      rm[nt].word = ~0u;
-      if (p.mask_mode == BSX_MASK_TREE && rv) rm[nt].word = p.mask_words[cur.qo_start + tq];
       if (has_tiles) {
         const uint16_t* qp =
             p.q + (int64_t)(cur.qo_start + tq) * p.q_stride + (int64_t)(h * g + hh) * D;
@@ -346,85 +568,14 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (PREFETCH) load_tile_k(pf_tile, pf_kv, pf_pages);
 
-      if constexpr (MASKED) {
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int j = j0 + 16 * st + 4 * g4 + e;
-            const int d = j - diag;
-            const bool in_view = (j < sink_end) | (j >= win_beg);
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-              const uint32_t bit = (rm[nt].word >> (uint32_t)min(max(d, 0), 31)) & 1u;
-              const bool vis = (j <= rm[nt].lim) & ((d < 0) | (bit != 0u)) & in_view;
-              sacc[st][nt][e] = vis ? sacc[st][nt][e] : -INFINITY;
-            }
-          }
-      }
+      if constexpr (MASKED) mask_tile<NT>(sacc, rm, j0, g4, diag, sink_end, win_beg);
 
-      // Softmax against the reference maximum m_ref (exp2 domain, scores scaled by
-      // scale_log2).  A rescale is needed only when some row's scaled maximum
-      // exceeds m_ref by more than the margin (always on the first visible tile).
-      bool need = false;
-      float tmax[NT];
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const float mx = fmaxf(fmaxf(fmaxf(sacc[0][nt][0], sacc[0][nt][1]),
-                                     fmaxf(sacc[0][nt][2], sacc[0][nt][3])),
-                               fmaxf(fmaxf(sacc[1][nt][0], sacc[1][nt][1]),
-                                     fmaxf(sacc[1][nt][2], sacc[1][nt][3])));
-        tmax[nt] = mx * p.scale_log2;
-        need |= tmax[nt] > m_ref[nt] + kRescaleMargin;
-      }
-      if (__builtin_amdgcn_ballot_w64(need) != 0) {
-        // wave-uniform and rare: row maxima over the 4 lane groups, then rescale
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          float mx = tmax[nt];
-          mx = fmaxf(mx, __shfl_xor(mx, 16));
-          mx = fmaxf(mx, __shfl_xor(mx, 32));
-          const float m_new = fmaxf(m_ref[nt], mx);
-          const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref[nt] - m_new);
-          l_run[nt] *= alpha;
-#pragma unroll
-          for (int jm = 0; jm < NJ; ++jm) o[jm][nt] *= alpha;
-          m_ref[nt] = m_new;
-        }
-      }
       uint32_t pb[NT][4];
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const float neg_m = m_ref[nt] == -INFINITY ? 0.f : -m_ref[nt];
-        float pv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[e >> 2][nt][e & 3], p.scale_log2, neg_m));
-          l_run[nt] += pv[e];
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pb[nt][r] = pack2<DT>(pv[2 * r], pv[2 * r + 1]);
-      }
+      softmax_tile<DT, NJ, NT>(sacc, p.scale_log2, m_ref, l_run, o, pb);
 
-      if constexpr (MASKED) {  // rows past kv_len hold unrelated data: zero them
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const bool ok = j0 + 16 * (e >> 2) + 4 * g4 + (e & 3) < cur.kv_len;
-#pragma unroll
-          for (int w = 0; w < VW; ++w) vraw[e][w] = ok ? vraw[e][w] : 0u;
-        }
-      }
-      // V^T operands: A_jm[e] = V[tau(g4, e)][NJ*c16 + jm]
+      if constexpr (MASKED) zero_rows_past_end<VW>(vraw, j0, g4, cur.kv_len);
       u32x4 va[NJ];
-#pragma unroll
-      for (int jm = 0; jm < NJ; ++jm) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t w0 = vraw[2 * r][jm >> 1];
-          const uint32_t w1 = vraw[2 * r + 1][jm >> 1];
-          va[jm][r] = (jm & 1) ? perm_hi(w0, w1) : perm_lo(w0, w1);
-        }
-      }
+      transpose_v<NJ, VW>(vraw, va);
       // The transposed operands must be complete before the V registers are refilled:
       // an empty asm that reads them (and orders memory) pins the transposes above the
       // prefetch so the loads land in place.
@@ -432,13 +583,7 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       for (int jm = 0; jm < NJ; ++jm) asm volatile("" ::"v"(va[jm]) : "memory");
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (PREFETCH) load_tile_v(pf_tile, pf_kv, pf_pages);  // V registers are free
-#pragma unroll
-      for (int jm = 0; jm < NJ; ++jm)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          u32x4 bop = {pb[nt][0], pb[nt][1], pb[nt][2], pb[nt][3]};
-          o[jm][nt] = mfma16x16x32<DT>(va[jm], bop, o[jm][nt]);
-        }
+      pv_tile<DT, NJ, NT>(va, pb, o);
     };
 
     if (has_tiles) {
@@ -462,76 +607,313 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       load_tile_v(end_tile, end_kv, end_pages);
     }
 
-    // ---- finalize: lane holds row c16 of tile nt, d = NJ*(4 g4 + e) + jm
-    float lse2[NT];
-    bool rowv[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float l = l_run[nt];
-      l += __shfl_xor(l, 16);
-      l += __shfl_xor(l, 32);
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-#pragma unroll
-      for (int jm = 0; jm < NJ; ++jm) o[jm][nt] *= inv;
-      lse2[nt] = l > 0.f ? m_ref[nt] + __log2f(l) : -INFINITY;
-      rowv[nt] = row0 + nt * 16 + c16 < nrows;
-    }
-
-    if (cur.slot >= 0) {
-      // Split request: publish this part for the merge kernel.  The normalised partial
-      // output is stored in bf16 (fp32's exponent range, so any input is safe; one
-      // extra rounding of 2^-9 relative), halving the partial traffic, which is
-      // written, flushed from L2 at kernel end and read back by the merge.  Plain
-      // stores: the pieces of a row combine into full lines in L2 (non-temporal
-      // stores measured 2.3x the write traffic).
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        if (!rowv[nt]) continue;
-        const int row = row0 + nt * 16 + c16;
-        const int64_t prow = ((int64_t)cur.slot * p.num_kv_heads + h) * p.qrows_total + row;
-        uint16_t* pp = p.part_o + prow * D + NJ * 4 * g4;
-        uint32_t packed[2 * NJ];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int jm = 0; jm < NJ; jm += 2)
-            packed[(NJ * e + jm) / 2] = pack2<BSX_DTYPE_BF16>(o[jm][nt][e], o[jm + 1][nt][e]);
-#pragma unroll
-        for (int w = 0; w < 2 * NJ; w += 4) {
-          u32x4 v = {packed[w], packed[w + 1], packed[w + 2], packed[w + 3]};
-          *reinterpret_cast<u32x4*>(pp + 2 * w) = v;
-        }
-        if (g4 == 0) p.part_lse[prow] = lse2[nt];
-      }
-    } else {
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        if (!rowv[nt]) continue;
-        const int row = row0 + nt * 16 + c16;
-        const int tq = row / g;
-        const int hh = row - tq * g;
-        uint16_t* op = p.out + (int64_t)(cur.qo_start + tq) * p.out_stride +
-                       (int64_t)(h * g + hh) * D + NJ * 4 * g4;
-        uint32_t packed[2 * NJ];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int jm = 0; jm < NJ; jm += 2)
-            packed[(NJ * e + jm) / 2] = pack2<DT>(o[jm][nt][e], o[jm + 1][nt][e]);
-#pragma unroll
-        for (int w = 0; w < 2 * NJ; w += 4) {
-          u32x4 v = {packed[w], packed[w + 1], packed[w + 2], packed[w + 3]};
-          *reinterpret_cast<u32x4*>(op + 2 * w) = v;
-        }
-        if (p.lse_out != nullptr && g4 == 0)
-          p.lse_out[(int64_t)(cur.qo_start + tq) * p.num_qo_heads + h * g + hh] =
-              lse2[nt] * 0.69314718055994531f;
-      }
-    }
+    finish_segment<DT, D, NT>(p, cur, h, row0, c16, g4, o, m_ref, l_run);
 
     cur = nxt;
     nxt = load_seg(p, min(si + 2, seg_end - 1));
   }
+}
+
+// ---- Shared K/V tiles -----------------------------------------------------------
+//
+// When a kv head has more query rows than one wave holds (long drafts, token trees,
+// large GQA groups), QB waves work on the same kv head.  Streaming its K/V tiles into
+// each of those waves' registers would multiply the vector-memory requests per byte by
+// QB, and the address/data path of the compute units, not HBM, would set the pace.
+// Instead every K/V tile is copied once into LDS by direct global->LDS loads, split
+// between the QB waves of the head, through a ring of tile stages; every wave then
+// reads its MFMA operands from LDS.  Ring protocol, per tile n (stage n mod S):
+//   wait until this wave's loads of tile n landed (at most (S-2) tiles of its loads
+//   younger than them are in flight), barrier (every wave's loads of tile n landed and
+//   every wave finished reading tile n-1), issue the loads of tile n+S-1 into the stage
+//   of tile n-1, compute tile n from LDS.
+// The direct loads are issued from inline assembly, invisible to the compiler's wait
+// counting (it would otherwise wait for every load in flight before any LDS read); the
+// wait above is explicit.  Loads return in issue order, so a count of younger loads
+// is exact, and any other load issued later only makes the wait stricter.
+template <int D>
+struct SharedTile {
+  static constexpr int kRowGranules = D / 8;        // 16-byte granules per token row
+  static constexpr int kHalfBytes = kTile * D * 2;  // K (or V) part of one head's tile
+  static constexpr int kHeadBytes = 2 * kHalfBytes;
+  static constexpr int kChunks = kHeadBytes / 1024;  // 1 KB direct loads per head tile
+  static constexpr int kLdsBytes = attn_shape::kSharedLdsBytes;
+  // Column swizzle: the lanes that read one column of 16 consecutive tokens (K
+  // operands) or one token row (V operands) fall into distinct 16-byte bank groups.
+  __device__ static __forceinline__ int swz(int t) {
+    return D == 128 ? (t & 15) : ((t & 7) ^ ((t >> 3) & 1));
+  }
+  // granule index of (token t, column c) inside a K or V half
+  __device__ static __forceinline__ int at(int t, int c) {
+    return t * kRowGranules + (c ^ swz(t));
+  }
+};
+
+// 64 lanes x 16 bytes from sbase + voff (per lane) into LDS bytes [lds, lds + 1024),
+// lane i at lds + 16 i.  M0 carries the LDS address (one wait state before its use).
+// Non-temporal: the tiles are read once (measured on MI355X: 7.3 TB/s streaming
+// through a 4-stage LDS ring, against 5.9 TB/s with the default policy).
+__device__ __forceinline__ void dma_1k(const char* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+               ::"s"(lds), "v"(voff), "s"(sbase)
+               : "memory");
+}
+
+template <int DT, int D, int QB>
+__global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
+  using L = SharedTile<D>;
+  constexpr int NT = 2;       // 32 query rows per wave
+  constexpr int KS = D / 32;  // k-steps of the QK^T contraction
+  constexpr int NJ = D / 16;  // output d tiles
+  constexpr int VW = NJ / 2;  // dwords per lane per token of a V row
+  constexpr int QT = 16 * NT;
+  constexpr int S = attn_shape::shared_stages(D, QB);
+  constexpr int NPER = L::kChunks / QB;  // direct loads per wave per tile
+  constexpr int WAIT = (S - 2) * NPER;
+  constexpr int HALF_CHUNKS = L::kChunks / 2;
+  static_assert(L::kChunks % QB == 0 && (S & (S - 1)) == 0, "bad shared-tile shape");
+
+  __shared__ __attribute__((aligned(1024))) u32x4 smem[L::kLdsBytes / 16];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = uni(threadIdx.x >> 6);  // scalar: the load addresses derive from it
+  const int c16 = lane & 15;
+  const int g4 = lane >> 4;
+  const int hs = wave / QB;  // head slot of the workgroup
+  const int qi = wave % QB;  // query block of the head
+  const int hgroup = blockIdx.y / p.n_qgroups;
+  const int qgroup = blockIdx.y % p.n_qgroups;
+  const int h = hgroup * p.heads_per_cta + hs;
+  const int row0 = (qgroup * QB + qi) * QT;
+
+  const int seg_begin = ld_uniform(p.blob, p.off_seg_indptr + blockIdx.x);
+  const int seg_end = ld_uniform(p.blob, p.off_seg_indptr + blockIdx.x + 1);
+  if (seg_begin >= seg_end) return;
+
+  const int g = p.group;
+  const uint32_t tok_bytes = (uint32_t)(p.num_kv_heads * D * 2);
+  const uint32_t head_off = (uint32_t)(h * D * 2);
+  const int stage_granules = p.heads_per_cta * (L::kHeadBytes / 16);
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
+
+  // ---- producer: this wave loads chunks [qi*NPER, (qi+1)*NPER) of its head's tile.
+  // Chunk c is 64 consecutive granules (slots) of the K (c < HALF_CHUNKS) or V half;
+  // slot s holds token s / kRowGranules, column (s % kRowGranules) ^ swz(token).
+  uint32_t lane_off[NPER];
+#pragma unroll
+  for (int r = 0; r < NPER; ++r) {
+    const int cc = (qi * NPER + r) % HALF_CHUNKS;
+    const int s = 64 * cc + lane;
+    const int t = s / L::kRowGranules;
+    const int col = (s % L::kRowGranules) ^ L::swz(t);
+    lane_off[r] = (uint32_t)(t & 15) * tok_bytes + head_off + (uint32_t)col * 16u;
+  }
+  // Schedule position of the next tile to load (segments without tiles are skipped;
+  // past the end, nothing is loaded), with the page ids of its two 16-token subtiles.
+  // The page ids are read when the cursor moves, one tile before the loads that use
+  // them: a scalar read issued right before the loads would put its latency (long
+  // under full memory load) on every tile's critical path.
+  int pr_si = seg_begin, pr_tile = 0, pr_t1 = 0, pr_kv = 0, pr_pages = 0;
+  int pr_page0 = 0, pr_page1 = 0;  // (scalars, not an array indexed by a
+  int pr_pofs0 = 0, pr_pofs1 = 0;  //  wave-dependent subtile: no dynamic indexing)
+  bool pr_valid = false;
+  auto pr_pages_of_tile = [&]() {
+    const int j0 = pr_tile * kTile;
+    const int js1 = j0 + 16;
+    const int jsc0 = j0 < pr_kv ? j0 : 0;  // subtile starts, clamped into the request
+    const int jsc1 = js1 < pr_kv ? js1 : 0;
+    pr_page0 = ld_uniform(p.kv_indices, pr_pages + (jsc0 >> p.page_shift));
+    pr_page1 = ld_uniform(p.kv_indices, pr_pages + (jsc1 >> p.page_shift));
+    pr_pofs0 = (int)((uint32_t)(jsc0 & p.page_mask) * tok_bytes);
+    pr_pofs1 = (int)((uint32_t)(jsc1 & p.page_mask) * tok_bytes);
+  };
+  auto pr_seek = [&](int si) {  // first segment >= si with tiles
+    pr_valid = false;
+    for (; si < seg_end; ++si) {
+      const Seg s = load_seg(p, si);
+      if (s.t0 < s.t1) {
+        pr_si = si;
+        pr_tile = s.t0;
+        pr_t1 = s.t1;
+        pr_kv = s.kv_len;
+        pr_pages = s.page_start;
+        pr_valid = true;
+        pr_pages_of_tile();
+        return;
+      }
+    }
+  };
+  auto pr_advance = [&]() {
+    if (!pr_valid) return;
+    if (++pr_tile >= pr_t1)
+      pr_seek(pr_si + 1);
+    else
+      pr_pages_of_tile();
+  };
+  auto pr_issue = [&](int stage) {
+    if (!pr_valid) return;
+    const uint32_t lds_stage =
+        lds_base + (uint32_t)((stage * stage_granules) * 16 + hs * L::kHeadBytes);
+#pragma unroll
+    for (int r = 0; r < NPER; ++r) {
+      const int c = qi * NPER + r;
+      const int half = c / HALF_CHUNKS;
+      const int cc = c % HALF_CHUNKS;
+      const int sub = (cc * 64 / L::kRowGranules) >> 4;  // subtile of the chunk's tokens
+      const int page = sub ? pr_page1 : pr_page0;
+      const uint32_t pofs = (uint32_t)(sub ? pr_pofs1 : pr_pofs0);
+      const char* base = (half ? p.v_cache : p.k_cache) + (int64_t)page * p.page_stride_bytes;
+      dma_1k(base, pofs + lane_off[r],
+             lds_stage + (uint32_t)(half * L::kHalfBytes + cc * 1024));
+    }
+  };
+
+  pr_seek(seg_begin);
+#pragma unroll
+  for (int k = 0; k < S - 1; ++k) {
+    pr_issue(k);
+    pr_advance();
+  }
+
+  // Lane parts of the LDS operand indices.  K: column chunk s of token c16 (the second
+  // 16-token subtile adds a constant); V: row 4 g4 + e4 (the second subtile likewise).
+  constexpr int SUBTILE = 16 * L::kRowGranules;  // granules of 16 token rows
+  int koff[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) koff[s] = L::at(c16, 4 * s + g4);
+  // V^T operands come from transposing LDS reads (ds_read_b64_tr_b16): in each group of
+  // 16 lanes, lane i receives element i & 3 of the 8 bytes addressed by lanes
+  // (i >> 2) + 4 k, k = 0..3.  Lane (c16, g4) therefore addresses token
+  // 16 h + 4 g4 + (c16 >> 2), columns 16 jm + 4 (c16 & 3) .. + 3, and receives
+  // V[16 h + 4 g4 + k][16 jm + c16]: A[m = c16][8 g4 + 4 h + k] of O^T += V^T P^T for
+  // output rows d = 16 jm + m (the token order of P^T, tau(g4, e) = 16 (e >> 2) +
+  // 4 g4 + (e & 3), matches).  vtr[jm]: 8-byte index; the second subtile (h = 1) adds
+  // a constant.
+  int vtr[NJ];
+#pragma unroll
+  for (int jm = 0; jm < NJ; ++jm)
+    vtr[jm] = 2 * L::at(4 * g4 + (c16 >> 2), 2 * jm + ((c16 & 3) >> 1)) + (c16 & 1);
+
+  int n = 0;  // tiles consumed so far (stage n mod S)
+  for (int si = seg_begin; si < seg_end; ++si) {
+    const Seg cur = load_seg(p, si);
+    const int nrows = cur.qo_len * g;
+    const bool has_tiles = cur.t0 < cur.t1;
+    const int diag = cur.kv_len - cur.qo_len;
+    const int sink_end = p.mask_mode == BSX_MASK_STREAMING ? p.sink : cur.kv_len;
+    const int win_beg = p.mask_mode == BSX_MASK_STREAMING ? cur.kv_len - p.window : cur.kv_len;
+    RowMask rm[NT];
+    row_masks<NT>(p, cur, row0, c16, rm);
+
+    // Q (B operand of S^T = K Q^T) in registers; padded rows read row 0.
+    u32x4 qr[NT * KS];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int row = row0 + nt * 16 + c16;
+      const bool rv = row < nrows;
+      const int tq = rv ? row / g : 0;
+      const int hh = rv ? row - tq * g : 0;
+      const uint16_t* qp =
+          p.q + (int64_t)(cur.qo_start + tq) * p.q_stride + (int64_t)(h * g + hh) * D;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        qr[nt * KS + s] = has_tiles ? *reinterpret_cast<const u32x4*>(qp + 32 * s + 8 * g4)
+                                    : u32x4{0u, 0u, 0u, 0u};
+    }
+    // Wait for Q and the mask words here, once per segment: a wait the compiler placed
+    // at their first use inside the tile loop would run on every tile and drain the
+    // direct loads in flight.
+#pragma unroll
+    for (int i = 0; i < NT * KS; ++i) asm volatile("" ::"v"(qr[i]));
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) asm volatile("" ::"v"(rm[nt].word));
+
+    f32x4 o[NJ][NT];
+#pragma unroll
+    for (int jm = 0; jm < NJ; ++jm)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[jm][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_ref[NT], l_run[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      m_ref[nt] = -INFINITY;
+      l_run[nt] = 0.f;
+    }
+
+    auto tile_step = [&](int tile, auto masked_tag) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      const int j0 = tile * kTile;
+      const int stage = n & (S - 1);
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(WAIT) : "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      pr_issue((stage + S - 1) & (S - 1));
+      pr_advance();
+
+      const u32x4* tk = smem + stage * stage_granules + hs * (L::kHeadBytes / 16);
+      const u32x4* tv = tk + L::kHalfBytes / 16;
+      f32x4 sacc[2][NT];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        u32x4 ka[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) ka[s] = tk[koff[s] + SUBTILE * st];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < KS; ++s) acc = mfma16x16x32<DT>(ka[s], qr[nt * KS + s], acc);
+          sacc[st][nt] = acc;
+        }
+      }
+      // V^T operands (issued before the softmax to hide the LDS latency)
+      u32x4 va[NJ];
+      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+      const lds_s16x4* tv8 = reinterpret_cast<const lds_s16x4*>(
+          reinterpret_cast<const __attribute__((address_space(3))) char*>(
+              (const __attribute__((address_space(3))) u32x4*)tv));
+#pragma unroll
+      for (int jm = 0; jm < NJ; ++jm) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            const_cast<lds_s16x4*>(tv8 + vtr[jm]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            const_cast<lds_s16x4*>(tv8 + vtr[jm] + 2 * SUBTILE));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+        const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+        va[jm] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+      }
+      if constexpr (MASKED) mask_tile<NT>(sacc, rm, j0, g4, diag, sink_end, win_beg);
+      uint32_t pb[NT][4];
+      softmax_tile<DT, NJ, NT>(sacc, p.scale_log2, m_ref, l_run, o, pb);
+      if constexpr (MASKED) {
+        // V rows of tokens at or past kv_len hold unrelated data: zero them (element
+        // e of va[jm] is token tau(g4, e))
+        uint32_t keep[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t0 = j0 + 16 * (r >> 1) + 4 * g4 + 2 * (r & 1);
+          keep[r] = (t0 < cur.kv_len ? 0x0000FFFFu : 0u) | (t0 + 1 < cur.kv_len ? 0xFFFF0000u : 0u);
+        }
+#pragma unroll
+        for (int jm = 0; jm < NJ; ++jm)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) va[jm][r] &= keep[r];
+      }
+      pv_tile<DT, NJ, NT>(va, pb, o);
+      ++n;
+    };
+
+    if (has_tiles) {
+      int limit = p.mask_mode == BSX_MASK_NONE ? cur.kv_len : diag;
+      if (p.mask_mode == BSX_MASK_STREAMING) limit = 0;
+      const int t_split = max(cur.t0, min(cur.t1, limit / kTile));
+      for (int tile = cur.t0; tile < t_split; ++tile) tile_step(tile, std::false_type());
+      for (int tile = t_split; tile < cur.t1; ++tile) tile_step(tile, std::true_type());
+    }
+    finish_segment<DT, D, NT, false>(p, cur, h, row0, c16, g4, o, m_ref, l_run);
+  }
+  // No direct load may still target this workgroup's LDS when it exits.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Combine the partial results of split requests: o = sum_p w_p o_p / sum_p w_p with
@@ -620,6 +1002,15 @@ static int launch_main(const bsx_attn_plan_t* plan, const Params& prm, int waves
   return BSX_OK;
 }
 
+template <int DT, int D, int QB>
+static int launch_shared(const bsx_attn_plan_t* plan, const Params& prm, hipStream_t st) {
+  dim3 grid(plan->num_ctas, (plan->num_kv_heads / plan->heads_per_cta) * prm.n_qgroups);
+  hipLaunchKernelGGL((verify_attn_shared_kernel<DT, D, QB>), grid,
+                     dim3(64 * plan->heads_per_cta * QB), 0, st, prm);
+  BSX_LAUNCH_CHECK();
+  return BSX_OK;
+}
+
 template <int DT, int D>
 static int launch_all(const bsx_attn_plan_t* plan, const Params& prm, hipStream_t st) {
   if (prm.safe_pos < 0) {
@@ -633,7 +1024,11 @@ static int launch_all(const bsx_attn_plan_t* plan, const Params& prm, hipStream_
   const int waves = plan->heads_per_cta * prm.qblocks_per_cta;
   const bool ps16 = plan->page_size >= 16;
   int rc;
-  if (plan->qrow_tile == 16) {
+  if (plan->shared_kv_tiles) {
+    rc = plan->qblocks_per_cta == 2   ? launch_shared<DT, D, 2>(plan, prm, st)
+         : plan->qblocks_per_cta == 4 ? launch_shared<DT, D, 4>(plan, prm, st)
+                                      : launch_shared<DT, D, 8>(plan, prm, st);
+  } else if (plan->qrow_tile == 16) {
     rc = ps16 ? launch_main<DT, D, 1, true>(plan, prm, waves, st)
               : launch_main<DT, D, 1, false>(plan, prm, waves, st);
   } else {
@@ -682,6 +1077,13 @@ extern "C" int bsx_attn_run(const bsx_attn_plan_t* plan, const int32_t* plan_blo
                   plan->heads_per_cta * plan->qblocks_per_cta <= 8 &&
                   plan->num_qgroups * plan->qblocks_per_cta >= plan->qrow_blocks,
               BSX_ERR_INVALID, "inconsistent plan (workgroup shape)");
+  if (plan->shared_kv_tiles) {
+    const int qb = plan->qblocks_per_cta;
+    BSX_REQUIRE((qb == 2 || qb == 4 || qb == 8) && plan->qrow_tile == 32 &&
+                    plan->page_size >= 16 &&
+                    attn_shape::shared_fits(plan->head_dim, qb, plan->heads_per_cta),
+                BSX_ERR_INVALID, "inconsistent plan (shared kv tiles)");
+  }
   if (plan->total_qo == 0) return BSX_OK;
 
   attn::Params prm;

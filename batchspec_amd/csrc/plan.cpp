@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "../../include/bsx.h"
+#include "attn_shape.h"
 
 namespace bsx {
 void set_error(const char* fmt, ...);
@@ -38,8 +39,8 @@ void set_error(const char* fmt, ...);
 
 namespace {
 
-constexpr int kTileTokens = 32;
-constexpr int kMaxWavesPerCta = 8;
+using bsx::attn_shape::kMaxWavesPerCta;
+using bsx::attn_shape::kTileTokens;
 // Cost of starting a segment, in kv tiles: the Q load of the new request (one memory
 // latency) and the write of its (partial) result, measured on MI355X at about two
 // tile times together.
@@ -155,19 +156,32 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   const int64_t max_rows = (int64_t)max_qo * group;
   const int qrow_tile = max_rows <= 16 ? 16 : 32;
   const int qrow_blocks = (int)std::max<int64_t>(1, (max_rows + qrow_tile - 1) / qrow_tile);
+  // Several waves per kv head: they share each K/V tile through LDS when a 16-token
+  // subtile always lies inside one page (the shared kernel's loads assume it).
+  const bool shared = qrow_blocks > 1 && page_size >= 16;
   int hpc = 1;  // kv heads per workgroup: largest divisor of num_kv_heads that fits
-  for (int c = 1; c <= num_kv_heads; ++c)
-    if (num_kv_heads % c == 0 && c * std::min(qrow_blocks, kMaxWavesPerCta) <= kMaxWavesPerCta)
-      hpc = c;
-  // Waves of one workgroup (the run side splits query blocks the same way).
-  int qbpc = qrow_blocks;
-  while (qbpc * hpc > kMaxWavesPerCta) qbpc = (qbpc + 1) / 2;
+  int qbpc;     // query blocks (waves) per kv head in one workgroup
+  if (shared) {
+    qbpc = qrow_blocks <= 2 ? 2 : qrow_blocks <= 4 ? 4 : 8;
+    for (int c = 1; c <= num_kv_heads; ++c)
+      if (num_kv_heads % c == 0 && c * qbpc <= kMaxWavesPerCta &&
+          bsx::attn_shape::shared_fits(head_dim, qbpc, c))
+        hpc = c;
+  } else {
+    for (int c = 1; c <= num_kv_heads; ++c)
+      if (num_kv_heads % c == 0 && c * std::min(qrow_blocks, kMaxWavesPerCta) <= kMaxWavesPerCta)
+        hpc = c;
+    qbpc = qrow_blocks;
+    while (qbpc * hpc > kMaxWavesPerCta) qbpc = (qbpc + 1) / 2;
+  }
   const int n_qgroups = (qrow_blocks + qbpc - 1) / qbpc;
   const int cta_waves = hpc * qbpc;
   // One grid row (blockIdx.y) per (kv-head group, query group); size grid.x so that
-  // all workgroups are resident at once on num_cus compute units (4 SIMDs each).
+  // all workgroups are resident at once on num_cus compute units (4 SIMDs each; the
+  // shared kernel's LDS ring allows one workgroup per compute unit).
   const int grid_y = (num_kv_heads / hpc) * n_qgroups;
-  const int resident_per_cu = std::max(1, 4 * waves_per_simd(head_dim, qrow_tile) / cta_waves);
+  const int resident_per_cu =
+      shared ? 1 : std::max(1, 4 * waves_per_simd(head_dim, qrow_tile) / cta_waves);
   const int num_ctas = std::max(1, (num_cus * resident_per_cu) / grid_y);
 
   // Work units: contiguous tile ranges per request (two for the sink+window view).
@@ -297,5 +311,6 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   out->total_qo = batch > 0 ? qo_indptr_h[batch] : 0;
   out->safe_page_pos = safe_pos;
   out->total_tiles = total_tiles;
+  out->shared_kv_tiles = shared ? 1 : 0;
   return BSX_OK;
 }

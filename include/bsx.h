@@ -97,7 +97,9 @@ typedef struct {
   int32_t total_qo;       /* qo_indptr[batch]                                 */
   int32_t safe_page_pos;  /* a kv_indices position owned by some request, or -1
                              when the page table holds no page               */
-  int32_t reserved;
+  int32_t shared_kv_tiles;/* 1: the qblocks_per_cta waves of a kv head share
+                             each K/V tile through LDS (many query rows per
+                             kv head); 0: every wave streams its own tiles   */
   int64_t total_tiles;    /* kv tiles of the whole schedule                   */
 } bsx_attn_plan_t;
 

@@ -83,6 +83,28 @@ def test_query_lengths(qo):
     check(out, oracle_out(b, "causal"))
 
 
+# Shapes with several waves per kv head (query rows > 32), which share each K/V tile
+# through LDS: (D, Hq, Hkv, qo, page size, dtype, ctx range, causal, waves per head).
+SHARED_CASES = [
+    (64, 32, 4, 12, 32, torch.float16, (100, 2000), True, 4),
+    (64, 16, 2, 40, 16, torch.bfloat16, (50, 1500), True, 8),   # two query groups
+    (128, 32, 8, 24, 64, torch.float16, (8000, 20000), True, 4),  # split + merge
+    (128, 32, 8, 33, 16, torch.bfloat16, (40, 3000), False, 8),
+    (128, 32, 8, 16, 16, torch.bfloat16, (1, 700), True, 2),
+]
+
+
+@pytest.mark.parametrize("case", range(len(SHARED_CASES)))
+def test_shared_kv_tiles(case):
+    D, Hq, Hkv, qo, ps, dtype, (lo, hi), causal, qb = SHARED_CASES[case]
+    say(f"shared kv tiles D={D} H={Hq}/{Hkv} qo={qo} ps={ps} {dtype} ctx=[{lo},{hi}] causal={causal}")
+    b = make_verify_batch(5, lo, hi, qo, Hq, Hkv, D, ps, dtype=dtype, scale=0.5,
+                          seed=300 + case).to(DEV)
+    out, w = run_gpu(b, causal=causal)
+    assert w.plan_info.shared_kv_tiles == 1 and w.plan_info.qblocks_per_cta == qb
+    check(out, oracle_out(b, "causal" if causal else "none"))
+
+
 def test_ragged_mixed_batch_with_empty_requests():
     say("ragged qo/ctx incl. qo=0 and kv=0")
     qo = np.array([5, 0, 1, 17, 5, 2, 0, 5])
