@@ -182,11 +182,14 @@ __device__ __forceinline__ void mask_tile(f32x4 (&sacc)[2][NT], const RowMask (&
 // Online softmax of one tile against the reference maximum m_ref (exp2 domain, scores
 // scaled by scale_log2).  The reference is raised, and O and l rescaled, only when some
 // row's scaled maximum exceeds it by more than the margin (always on the first visible
-// tile).  Returns the probabilities packed as the B operand of O^T += V^T P^T.
-template <int DT, int NJ, int NT>
+// tile).  Returns the probabilities packed as the B operand of O^T += V^T P^T.  The row
+// sums go to l_run (this lane's share) or, with MMA_L, are left to the caller's matrix
+// accumulator lacc (rescaled here with O).
+template <int DT, int NJ, int NT, bool MMA_L = false>
 __device__ __forceinline__ void softmax_tile(const f32x4 (&sacc)[2][NT], float scale_log2,
                                              float (&m_ref)[NT], float (&l_run)[NT],
-                                             f32x4 (&o)[NJ][NT], uint32_t (&pb)[NT][4]) {
+                                             f32x4 (&o)[NJ][NT], uint32_t (&pb)[NT][4],
+                                             f32x4* lacc = nullptr) {
   bool need = false;
   float tmax[NT];
 #pragma unroll
@@ -206,7 +209,10 @@ __device__ __forceinline__ void softmax_tile(const f32x4 (&sacc)[2][NT], float s
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_ref[nt], mx);
       const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref[nt] - m_new);
-      l_run[nt] *= alpha;
+      if constexpr (MMA_L)
+        lacc[nt] *= alpha;
+      else
+        l_run[nt] *= alpha;
 #pragma unroll
       for (int jm = 0; jm < NJ; ++jm) o[jm][nt] *= alpha;
       m_ref[nt] = m_new;
@@ -219,7 +225,7 @@ __device__ __forceinline__ void softmax_tile(const f32x4 (&sacc)[2][NT], float s
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[e >> 2][nt][e & 3], scale_log2, neg_m));
-      l_run[nt] += pv[e];
+      if constexpr (!MMA_L) l_run[nt] += pv[e];
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) pb[nt][r] = pack2<DT>(pv[2 * r], pv[2 * r + 1]);
@@ -296,7 +302,9 @@ __device__ __forceinline__ void store_row(uint16_t* dst, int g4, const f32x4 (&o
   }
 }
 
-template <int DT, int D, int NT, bool INTERLEAVED = true>
+// l_run: this lane's share of the row sums (summed over the 4 lane groups here), or,
+// with L_COMPLETE, the whole row sums.
+template <int DT, int D, int NT, bool INTERLEAVED = true, bool L_COMPLETE = false>
 __device__ __forceinline__ void finish_segment(const Params& p, const Seg& cur, int h, int row0,
                                                int c16, int g4, f32x4 (&o)[D / 16][NT],
                                                const float (&m_ref)[NT],
@@ -309,8 +317,10 @@ __device__ __forceinline__ void finish_segment(const Params& p, const Seg& cur, 
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     float l = l_run[nt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    if constexpr (!L_COMPLETE) {
+      l += __shfl_xor(l, 16);
+      l += __shfl_xor(l, 32);
+    }
     const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
     for (int jm = 0; jm < NJ; ++jm) o[jm][nt] *= inv;
@@ -637,11 +647,13 @@ struct SharedTile {
   static constexpr int kHalfBytes = kTile * D * 2;  // K (or V) part of one head's tile
   static constexpr int kHeadBytes = 2 * kHalfBytes;
   static constexpr int kChunks = kHeadBytes / 1024;  // 1 KB direct loads per head tile
-  static constexpr int kLdsBytes = attn_shape::kSharedLdsBytes;
-  // Column swizzle: the lanes that read one column of 16 consecutive tokens (K
-  // operands) or one token row (V operands) fall into distinct 16-byte bank groups.
+  // Column swizzle (XOR of the 16-byte column with a linear function of the token):
+  // the 8 or 16 lanes served together by the LDS fall into distinct 16-byte bank
+  // groups, both for the K reads (one column of 16 consecutive tokens) and for the
+  // transposing V reads (two columns of 4 consecutive tokens per 16 lanes).
   __device__ static __forceinline__ int swz(int t) {
-    return D == 128 ? (t & 15) : ((t & 7) ^ ((t >> 3) & 1));
+    if constexpr (D == 128) return (t & 15) ^ ((t & 1) << 3);
+    return ((t >> 1) & 3) | (((t ^ (t >> 1) ^ (t >> 3)) & 1) << 2);
   }
   // granule index of (token t, column c) inside a K or V half
   __device__ static __forceinline__ int at(int t, int c) {
@@ -673,7 +685,7 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
   constexpr int HALF_CHUNKS = L::kChunks / 2;
   static_assert(L::kChunks % QB == 0 && (S & (S - 1)) == 0, "bad shared-tile shape");
 
-  __shared__ __attribute__((aligned(1024))) u32x4 smem[L::kLdsBytes / 16];
+  __shared__ __attribute__((aligned(1024))) u32x4 smem[attn_shape::shared_lds_bytes(D, QB) / 16];
 
   const int lane = threadIdx.x & 63;
   const int wave = uni(threadIdx.x >> 6);  // scalar: the load addresses derive from it
@@ -834,11 +846,17 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) o[jm][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_ref[NT], l_run[NT];
+    // Row sums on the matrix core: lacc[nt] += ONES P^T, every element of lane
+    // (c16, g4) is the sum for row c16 (of the same 16-bit P the output uses).
+    f32x4 lacc[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       m_ref[nt] = -INFINITY;
       l_run[nt] = 0.f;
+      lacc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    constexpr uint32_t kOne2 = DT == BSX_DTYPE_BF16 ? 0x3F803F80u : 0x3C003C00u;
+    const u32x4 ones = {kOne2, kOne2, kOne2, kOne2};
 
     auto tile_step = [&](int tile, auto masked_tag) {
       constexpr bool MASKED = decltype(masked_tag)::value;
@@ -884,7 +902,7 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
       }
       if constexpr (MASKED) mask_tile<NT>(sacc, rm, j0, g4, diag, sink_end, win_beg);
       uint32_t pb[NT][4];
-      softmax_tile<DT, NJ, NT>(sacc, p.scale_log2, m_ref, l_run, o, pb);
+      softmax_tile<DT, NJ, NT, true>(sacc, p.scale_log2, m_ref, l_run, o, pb, lacc);
       if constexpr (MASKED) {
         // V rows of tokens at or past kv_len hold unrelated data: zero them (element
         // e of va[jm] is token tau(g4, e))
@@ -900,6 +918,11 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
           for (int r = 0; r < 4; ++r) va[jm][r] &= keep[r];
       }
       pv_tile<DT, NJ, NT>(va, pb, o);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        u32x4 bop = {pb[nt][0], pb[nt][1], pb[nt][2], pb[nt][3]};
+        lacc[nt] = mfma16x16x32<DT>(ones, bop, lacc[nt]);
+      }
       ++n;
     };
 
@@ -910,7 +933,9 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
       for (int tile = cur.t0; tile < t_split; ++tile) tile_step(tile, std::false_type());
       for (int tile = t_split; tile < cur.t1; ++tile) tile_step(tile, std::true_type());
     }
-    finish_segment<DT, D, NT, false>(p, cur, h, row0, c16, g4, o, m_ref, l_run);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) l_run[nt] = lacc[nt][0];
+    finish_segment<DT, D, NT, false, true>(p, cur, h, row0, c16, g4, o, m_ref, l_run);
   }
   // No direct load may still target this workgroup's LDS when it exits.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1081,7 +1106,7 @@ extern "C" int bsx_attn_run(const bsx_attn_plan_t* plan, const int32_t* plan_blo
     const int qb = plan->qblocks_per_cta;
     BSX_REQUIRE((qb == 2 || qb == 4 || qb == 8) && plan->qrow_tile == 32 &&
                     plan->page_size >= 16 &&
-                    attn_shape::shared_fits(plan->head_dim, qb, plan->heads_per_cta),
+                    plan->heads_per_cta <= attn_shape::shared_max_heads(plan->head_dim, qb),
                 BSX_ERR_INVALID, "inconsistent plan (shared kv tiles)");
   }
   if (plan->total_qo == 0) return BSX_OK;

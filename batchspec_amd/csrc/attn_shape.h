@@ -7,18 +7,20 @@ namespace attn_shape {
 
 constexpr int kTileTokens = 32;     // kv tokens per inner-loop tile
 constexpr int kMaxWavesPerCta = 8;
-constexpr int kSharedLdsBytes = 128 * 1024;  // LDS of the shared-tile kernel
+constexpr int kLdsPerCu = 160 * 1024;
 
 // Bytes of one kv head's K and V tile.
 constexpr int head_tile_bytes(int head_dim) { return 2 * kTileTokens * head_dim * 2; }
 
-// Ring depth of the shared-tile kernel with qb waves per kv head: the deepest ring
-// that holds 8 / qb heads in kSharedLdsBytes.
+// Shared-tile kernel with qb waves per kv head: at most shared_max_heads kv heads per
+// workgroup, a ring of shared_stages tile stages.  Adjacent kv heads share a
+// workgroup: the DRAM channels of a head's 256-byte slices of the token rows depend on
+// the head (measured on MI355X: one fixed head per workgroup streams at 6.4 TB/s,
+// two adjacent heads at 6.7 TB/s), and a workgroup's pace follows its slices.
+constexpr int shared_max_heads(int head_dim, int qb) { return 8 / qb; }
 constexpr int shared_stages(int head_dim, int qb) { return (head_dim == 128 && qb == 2) ? 2 : 4; }
-
-// Whether a workgroup of `heads` kv heads fits the shared-tile kernel's LDS.
-constexpr bool shared_fits(int head_dim, int qb, int heads) {
-  return shared_stages(head_dim, qb) * heads * head_tile_bytes(head_dim) <= kSharedLdsBytes;
+constexpr int shared_lds_bytes(int head_dim, int qb) {
+  return shared_stages(head_dim, qb) * shared_max_heads(head_dim, qb) * head_tile_bytes(head_dim);
 }
 
 }  // namespace attn_shape

@@ -164,8 +164,7 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   if (shared) {
     qbpc = qrow_blocks <= 2 ? 2 : qrow_blocks <= 4 ? 4 : 8;
     for (int c = 1; c <= num_kv_heads; ++c)
-      if (num_kv_heads % c == 0 && c * qbpc <= kMaxWavesPerCta &&
-          bsx::attn_shape::shared_fits(head_dim, qbpc, c))
+      if (num_kv_heads % c == 0 && c <= bsx::attn_shape::shared_max_heads(head_dim, qbpc))
         hpc = c;
   } else {
     for (int c = 1; c <= num_kv_heads; ++c)
@@ -178,10 +177,13 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   const int cta_waves = hpc * qbpc;
   // One grid row (blockIdx.y) per (kv-head group, query group); size grid.x so that
   // all workgroups are resident at once on num_cus compute units (4 SIMDs each; the
-  // shared kernel's LDS ring allows one workgroup per compute unit).
+  // shared kernel's LDS ring also bounds its workgroups per compute unit).
   const int grid_y = (num_kv_heads / hpc) * n_qgroups;
-  const int resident_per_cu =
-      shared ? 1 : std::max(1, 4 * waves_per_simd(head_dim, qrow_tile) / cta_waves);
+  int resident_per_cu = std::max(1, 4 * waves_per_simd(head_dim, qrow_tile) / cta_waves);
+  if (shared)
+    resident_per_cu = std::max(
+        1, std::min(resident_per_cu,
+                    bsx::attn_shape::kLdsPerCu / bsx::attn_shape::shared_lds_bytes(head_dim, qbpc)));
   const int num_ctas = std::max(1, (num_cus * resident_per_cu) / grid_y);
 
   // Work units: contiguous tile ranges per request (two for the sink+window view).
