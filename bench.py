@@ -280,11 +280,12 @@ def main() -> int:
                                    "frac": round(gbytes / t_acc / 1e3 / HBM_PEAK_GBS, 4)}
         result["verify_step_32_layers_us"] = round(t_model, 1)
         # accepted-KV compaction (collate_accepted_kv_cache) of the same accept counts over
-        # the three config-2 caches taken as three layers: rows prev + i*(k+1) -> prev + i
+        # three layers of config-2 shape (set 0's cache and two more of its shape; layers
+        # share one page table): rows prev + i*(k+1) -> prev + i
         from batchspec_amd.collate import collate_accepted_kv_cache
         kvl = torch.from_numpy(np.ascontiguousarray(sets[0].kv_lens)).to(dev)
         prev = (kvl - 25).to(torch.int32)
-        caches = [b.cache for b in sets]
+        caches = [sets[0].cache] + [torch.empty_like(sets[0].cache) for _ in range(2)]
         col_us = time_events(lambda i: collate_accepted_kv_cache(
             acc_ref, prev, 4, caches, sets[0].kv_indptr, sets[0].kv_indices), args.steps, 3)
         t_col = sum(col_us) / len(col_us)
@@ -292,7 +293,7 @@ def main() -> int:
         result["collate_accepted_kv"] = {"us_3_layers": round(t_col, 2),
                                          "bytes_moved": moved,
                                          "GB/s": round(moved / t_col / 1e3, 1)}
-        del gl, g
+        del gl, g, caches
         # stochastic acceptance (config 5)
         s = stochastic_case(device=dev)
         st_us = time_events(lambda i: bsx.sampling.chain_speculative_sampling_from_logits(
