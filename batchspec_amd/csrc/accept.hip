@@ -460,27 +460,31 @@ __global__ void __launch_bounds__(256) softmax_norm_kernel(const void* logits, i
 // ----------------------------------------------------------------------------
 // Argmax (torch semantics: the first maximum wins, NaN counts as the maximum).
 //
-// One streaming pass over the flattened [rows, V] logits, cut into equal chunks of
-// elements regardless of row boundaries (every workgroup does the same work), then a
-// small combine.  A thread visits its columns in increasing order, so ties keep the
-// earlier column with a strict comparison; each 8-element vector costs one
-// NaN-propagating maximum3 reduction and a compare, and only a new maximum (rare
-// after the first few vectors) takes the branch that locates its first column.
+// Every row is cut into `parts` equal column ranges, one workgroup each, sized so that
+// a thread issues all of its loads of the range at once (one memory round trip per
+// workgroup, and every workgroup of a [320, 128256] call resident at the same time),
+// then a small combine over the parts of a row in column order.  A thread visits its
+// columns in increasing order, so ties keep the earlier column with a strict
+// comparison; each 8-element vector costs a NaN-propagating maximum reduction and a
+// branch-free update of (running maximum, vector holding it), and the column inside
+// the winning vector is located once, from registers.
 // ----------------------------------------------------------------------------
+constexpr int kArgmaxThreads = 256;
+constexpr int kArgmaxBytesPerThread = 256;  // loads in flight per thread
+
 struct ArgmaxSplit {
-  int64_t n;      // rows * V
-  int64_t chunk;  // elements per workgroup (multiple of 8)
-  int64_t w;      // workgroups
-  int maxp;       // row pieces one workgroup can touch
+  int64_t parts;  // workgroups per row
+  int64_t chunk;  // columns per workgroup (multiple of 8)
 };
 
-static ArgmaxSplit argmax_split(int64_t rows, int64_t V) {
+static ArgmaxSplit argmax_split(int64_t rows, int64_t V, int elem_bytes) {
+  const int64_t cols_per_wg = (int64_t)kArgmaxThreads * kArgmaxBytesPerThread / elem_bytes;
+  int64_t parts = ceil_div(V, cols_per_wg);
+  // few rows: more, smaller parts (at least ~512 workgroups, parts of >= 4096 columns)
+  parts = std::max(parts, std::min(ceil_div(V, 4096), ceil_div(512, std::max<int64_t>(rows, 1))));
   ArgmaxSplit a;
-  a.n = rows * V;
-  int64_t w = std::max<int64_t>(1, std::min<int64_t>(8192, ceil_div(a.n, 81920)));
-  a.chunk = ceil_div(ceil_div(a.n, w), 8) * 8;
-  a.w = ceil_div(a.n, a.chunk);
-  a.maxp = (int)(a.chunk / V) + 2;
+  a.chunk = ceil_div(ceil_div(V, parts), 8) * 8;
+  a.parts = ceil_div(V, a.chunk);
   return a;
 }
 
@@ -501,40 +505,42 @@ __device__ __forceinline__ void take(float x, int col, float& bv, int& bc) {
   }
 }
 
+// The 8 values of a vector as fp32.
 template <int DT>
-__device__ __forceinline__ void take8(const u32x4* p, int col, float& bv, int& bc) {
-  float x[8];
+__device__ __forceinline__ void vec8(const u32x4* p, float (&x)[8]) {
   if constexpr (DT == BSX_DTYPE_FP32) {
-    const f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
-    const f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+    const f32x4 a = __builtin_bit_cast(f32x4, p[0]);
+    const f32x4 b = __builtin_bit_cast(f32x4, p[1]);
     x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
     x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
   } else {
-    const u32x4 w = *p;
+    const u32x4 w = p[0];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       x[2 * q] = lo_f32<DT>(w[q]);
       x[2 * q + 1] = hi_f32<DT>(w[q]);
     }
   }
-  const float m = __builtin_elementwise_maximum(
+}
+
+__device__ __forceinline__ float max8(const float (&x)[8]) {
+  return __builtin_elementwise_maximum(
       __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[0], x[1]),
                                     __builtin_elementwise_maximum(x[2], x[3])),
       __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[4], x[5]),
                                     __builtin_elementwise_maximum(x[6], x[7])));
-  const bool upd = (bc == INT_MAX) || (m > bv) || ((m != m) && (bv == bv));
-  if (upd) {
-    int e = 7;
-#pragma unroll
-    for (int q = 6; q >= 0; --q)
-      if (x[q] == m || (m != m && x[q] != x[q])) e = q;
-    bv = m;
-    bc = col + e;
-  }
 }
 
-// Reduce (bv, bc) over the 512-thread workgroup; every thread gets the result.
-constexpr int kArgmaxThreads = 512;
+// First position in x of the value m (NaN matches NaN).
+__device__ __forceinline__ int first_of(const float (&x)[8], float m) {
+  int e = 7;
+#pragma unroll
+  for (int q = 6; q >= 0; --q)
+    if (x[q] == m || (m != m && x[q] != x[q])) e = q;
+  return e;
+}
+
+// Reduce (bv, bc) over the workgroup; every thread gets the result.
 __device__ __forceinline__ void block_best(float& bv, int& bc) {
   constexpr int NW = kArgmaxThreads / 64;
   __shared__ float s_v[NW];
@@ -564,84 +570,103 @@ __device__ __forceinline__ void block_best(float& bv, int& bc) {
     }
 }
 
+// grid rows * parts: workgroup (r, p) takes columns [p*chunk, min(V, (p+1)*chunk)) of row r.
+// (Evaluating the greedy acceptance inside this launch, by the workgroup that finishes
+// last, was measured slower on MI355X than the separate small kernel: the partials must
+// cross the XCDs' separate L2 caches, by a release fence per workgroup (an L2 write-back
+// each) or by written-through stores and uncached reads.)
 template <int DT>
-__global__ void __launch_bounds__(kArgmaxThreads) argmax_split_kernel(const void* logits, int64_t V,
-                                                           int64_t row_stride, int64_t n,
-                                                           int64_t chunk, int maxp, float* pval,
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_part_kernel(const void* logits, int64_t V,
+                                                           int64_t row_stride, int64_t parts,
+                                                           int64_t chunk, float* pval,
                                                            int32_t* pcol) {
   constexpr int ES = DT == BSX_DTYPE_FP32 ? 4 : 2;
-  const int64_t e0 = (int64_t)blockIdx.x * chunk;
-  const int64_t e1 = min(n, e0 + chunk);
+  constexpr int VW = ES / 2;  // 16-byte loads per 8-element vector
+  constexpr int NT = kArgmaxThreads;
+  constexpr int U = kArgmaxBytesPerThread / (16 * VW);  // vectors per thread per batch
+  const int64_t wg = blockIdx.x;
+  const int64_t r = wg / parts;
+  const int64_t part = wg - r * parts;
+  const int64_t c0 = part * chunk;
+  const int64_t c1 = min(V, c0 + chunk);
   const int t = threadIdx.x;
-  int piece = 0;
-  for (int64_t s = e0; s < e1; ++piece) {
-    const int64_t r = s / V;
-    const int64_t c0 = s - r * V;
-    const int64_t c1 = min(V, c0 + (e1 - s));
-    const char* row = static_cast<const char*>(logits) + r * row_stride * ES;
-    float bv = -INFINITY;
-    int bc = INT_MAX;
-    // head (unaligned), body (8-element vectors), tail: each thread's columns ascend
-    int64_t a0 = c0, a1 = c0;
-    if ((((uintptr_t)row) % 16) == 0) {
-      a0 = min(c1, (c0 + 7) / 8 * 8);
-      a1 = max(a0, c1 / 8 * 8);
+  const char* row = static_cast<const char*>(logits) + r * row_stride * ES;
+  float bv = -INFINITY;
+  int bc = INT_MAX;
+  // head (unaligned), body (8-element vectors), tail: each thread's columns ascend
+  int64_t a0 = c0, a1 = c0;
+  if ((((uintptr_t)row) % 16) == 0) {
+    a0 = min(c1, (c0 + 7) / 8 * 8);
+    a1 = max(a0, c1 / 8 * 8);
+  }
+  if (c0 + t < a0) take(load_one<DT>(row, c0 + t), (int)(c0 + t), bv, bc);
+  const int64_t nv = (a1 - a0) / 8;
+  const u32x4* vbase = reinterpret_cast<const u32x4*>(row + a0 * ES);
+  // The logits are read once: non-temporal loads, all U vectors of a batch issued
+  // together (indices past the range are clamped to its last vector and not used).
+  for (int64_t v0 = 0; v0 < nv; v0 += (int64_t)U * NT) {
+    u32x4 buf[U][VW];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t v = min(v0 + t + (int64_t)u * NT, nv - 1);
+#pragma unroll
+      for (int h = 0; h < VW; ++h) buf[u][h] = __builtin_nontemporal_load(vbase + v * VW + h);
     }
-    constexpr int NT = kArgmaxThreads;
-    if (c0 + t < a0) take(load_one<DT>(row, c0 + t), (int)(c0 + t), bv, bc);
-    const int64_t nv = (a1 - a0) / 8;
-    const u32x4* vbase = reinterpret_cast<const u32x4*>(row + a0 * ES);
-    // the logits are read once: non-temporal loads, 8 vectors in flight per thread
-    constexpr int U = 8 / (ES / 2);
-    int64_t v = t;
-    for (; v + (U - 1) * NT < nv; v += U * NT) {
-      u32x4 buf[U][ES / 2];
+    // running maximum of the batch and the first vector holding it (vectors arrive in
+    // increasing column order: strict rule, NaN sticks once seen); no branches
+    float m = bv;
+    int bu = -1;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float x[8];
+      vec8<DT>(buf[u], x);
+      const float m8 = max8(x);
+      const bool ok = v0 + t + (int64_t)u * NT < nv;
+      const bool upd = ok && ((bc == INT_MAX && bu < 0) || (m8 > m) || ((m8 != m8) && (m == m)));
+      m = upd ? m8 : m;
+      bu = upd ? u : bu;
+    }
+    if (bu >= 0) {  // locate the column inside the winning vector (registers only)
+      float x[8];
 #pragma unroll
       for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int h = 0; h < ES / 2; ++h)
-          buf[u][h] = __builtin_nontemporal_load(vbase + (v + u * NT) * (ES / 2) + h);
-#pragma unroll
-      for (int u = 0; u < U; ++u) take8<DT>(buf[u], (int)(a0 + 8 * (v + u * NT)), bv, bc);
+        if (u == bu) vec8<DT>(buf[u], x);
+      bv = m;
+      bc = (int)(a0 + 8 * (v0 + t + (int64_t)bu * NT)) + first_of(x, m);
     }
-    for (; v < nv; v += NT) take8<DT>(vbase + v * (ES / 2), (int)(a0 + 8 * v), bv, bc);
-    for (int64_t c = a1 + t; c < c1; c += NT) take(load_one<DT>(row, c), (int)c, bv, bc);
-    block_best(bv, bc);
-    if (t == 0) {
-      pval[(int64_t)blockIdx.x * maxp + piece] = bv;
-      pcol[(int64_t)blockIdx.x * maxp + piece] = bc;
-    }
-    s += c1 - c0;
+  }
+  for (int64_t c = a1 + t; c < c1; c += NT) take(load_one<DT>(row, c), (int)c, bv, bc);
+  block_best(bv, bc);
+  if (t == 0) {
+    pval[wg] = bv;
+    pcol[wg] = bc;
   }
 }
 
-// argmax of row r from the partials of the workgroups whose chunks cover it (the
-// first four loaded together, any further ones after).
+// argmax of row r from the partials of its parts, combined in column order.
 __device__ __forceinline__ int64_t row_argmax(const float* pval, const int32_t* pcol, int64_t r,
-                                              int64_t V, int64_t chunk, int maxp) {
-  const int64_t w0 = (r * V) / chunk;
-  const int64_t w1 = ((r + 1) * V - 1) / chunk;
-  float v[4];
-  int c[4];
+                                              int64_t parts) {
+  // the first 8 parts in one round of loads, any further ones after
+  constexpr int P = 8;
+  float v[P];
+  int c[P];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int64_t w = min(w0 + q, w1);
-    const int64_t piece = r - (w * chunk) / V;
-    v[q] = pval[w * maxp + piece];
-    c[q] = pcol[w * maxp + piece];
+  for (int q = 0; q < P; ++q) {
+    const int64_t i = r * parts + min((int64_t)q, parts - 1);
+    v[q] = pval[i];
+    c[q] = pcol[i];
   }
   float bv = v[0];
   int bc = c[0];
 #pragma unroll
-  for (int q = 1; q < 4; ++q)
-    if (better(v[q], c[q], bv, bc)) {
+  for (int q = 1; q < P; ++q)
+    if (q < parts && better(v[q], c[q], bv, bc)) {
       bv = v[q];
       bc = c[q];
     }
-  for (int64_t w = w0 + 4; w <= w1; ++w) {
-    const int64_t piece = r - (w * chunk) / V;
-    const float x = pval[w * maxp + piece];
-    const int cx = pcol[w * maxp + piece];
+  for (int64_t q = P; q < parts; ++q) {
+    const float x = pval[r * parts + q];
+    const int cx = pcol[r * parts + q];
     if (better(x, cx, bv, bc)) {
       bv = x;
       bc = cx;
@@ -650,25 +675,25 @@ __device__ __forceinline__ int64_t row_argmax(const float* pval, const int32_t* 
   return bc;
 }
 
-__global__ void argmax_final_kernel(const float* pval, const int32_t* pcol, int64_t rows, int64_t V,
-                                    int64_t chunk, int maxp, int64_t* out) {
+__global__ void argmax_final_kernel(const float* pval, const int32_t* pcol, int64_t rows,
+                                    int64_t parts, int64_t* out) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r < rows) out[r] = row_argmax(pval, pcol, r, V, chunk, maxp);
+  if (r < rows) out[r] = row_argmax(pval, pcol, r, parts);
 }
 
 // One wave per request: lane i < k+1 owns row (b, i); the evaluation of
 // mtp_engine.py:553-560 runs on ballots and shuffles.
 __global__ void __launch_bounds__(256) greedy_eval_kernel(
     const int64_t* draft, const int64_t* target_ids, const float* pval, const int32_t* pcol,
-    int64_t V, int64_t chunk, int maxp, int B, int k, int64_t eos, int mode, int64_t* bonus,
-    int64_t* accept, uint8_t* eos_acc) {
+    int64_t parts, int B, int k, int64_t eos, int mode, int64_t* bonus, int64_t* accept,
+    uint8_t* eos_acc) {
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (b >= B) return;
   const int i = threadIdx.x & 63;
   int64_t pred = -1;
   if (i <= k) {
     const int64_t r = (int64_t)b * (k + 1) + i;
-    pred = target_ids ? target_ids[r] : row_argmax(pval, pcol, r, V, chunk, maxp);
+    pred = target_ids ? target_ids[r] : row_argmax(pval, pcol, r, parts);
   }
   const int64_t d = i < k ? draft[(int64_t)b * k + i] : -2;
   const bool flag = i < k && pred == d;
@@ -693,21 +718,24 @@ __global__ void __launch_bounds__(256) greedy_eval_kernel(
   }
 }
 
-static int dispatch_argmax_split(const void* logits, int dtype, int64_t rows, int64_t V,
+static int elem_bytes_of(int dtype) { return dtype == BSX_DTYPE_FP32 ? 4 : 2; }
+
+static int dispatch_argmax_parts(const void* logits, int dtype, int64_t rows, int64_t V,
                                  int64_t stride, const ArgmaxSplit& sp, float* pv, int32_t* pc,
                                  hipStream_t st) {
+  const dim3 grid((unsigned)(rows * sp.parts));
   switch (dtype) {
     case BSX_DTYPE_BF16:
-      hipLaunchKernelGGL((argmax_split_kernel<BSX_DTYPE_BF16>), dim3((unsigned)sp.w), dim3(kArgmaxThreads), 0,
-                         st, logits, V, stride, sp.n, sp.chunk, sp.maxp, pv, pc);
+      hipLaunchKernelGGL((argmax_part_kernel<BSX_DTYPE_BF16>), grid, dim3(kArgmaxThreads), 0, st,
+                         logits, V, stride, sp.parts, sp.chunk, pv, pc);
       break;
     case BSX_DTYPE_FP16:
-      hipLaunchKernelGGL((argmax_split_kernel<BSX_DTYPE_FP16>), dim3((unsigned)sp.w), dim3(kArgmaxThreads), 0,
-                         st, logits, V, stride, sp.n, sp.chunk, sp.maxp, pv, pc);
+      hipLaunchKernelGGL((argmax_part_kernel<BSX_DTYPE_FP16>), grid, dim3(kArgmaxThreads), 0, st,
+                         logits, V, stride, sp.parts, sp.chunk, pv, pc);
       break;
     case BSX_DTYPE_FP32:
-      hipLaunchKernelGGL((argmax_split_kernel<BSX_DTYPE_FP32>), dim3((unsigned)sp.w), dim3(kArgmaxThreads), 0,
-                         st, logits, V, stride, sp.n, sp.chunk, sp.maxp, pv, pc);
+      hipLaunchKernelGGL((argmax_part_kernel<BSX_DTYPE_FP32>), grid, dim3(kArgmaxThreads), 0, st,
+                         logits, V, stride, sp.parts, sp.chunk, pv, pc);
       break;
     default:
       set_error("unknown dtype %d", dtype);
@@ -724,10 +752,21 @@ static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 using namespace bsx;
 
+// Partials of one (row, part) pair each; sized for fp32 logits, whose split has the
+// most parts, so one workspace serves every dtype.
+static int64_t argmax_partials(int64_t rows, int64_t vocab) {
+  return rows * acc::argmax_split(rows, vocab, 4).parts;
+}
+
+// Workspace: [partial values][partial columns].
+static int64_t argmax_values_offset() { return 0; }
+static int64_t argmax_columns_offset(int64_t rows, int64_t vocab) {
+  return acc::align256(argmax_partials(rows, vocab) * 4);
+}
+
 extern "C" int64_t bsx_argmax_ws_bytes(int64_t rows, int64_t vocab) {
   if (rows <= 0 || vocab <= 0) return 256;
-  const acc::ArgmaxSplit sp = acc::argmax_split(rows, vocab);
-  return acc::align256(sp.w * sp.maxp * 4) + sp.w * sp.maxp * 4;
+  return argmax_columns_offset(rows, vocab) + argmax_partials(rows, vocab) * 4;
 }
 
 extern "C" int bsx_argmax(const void* logits_d, int dtype, int64_t rows, int64_t vocab,
@@ -740,14 +779,18 @@ extern "C" int bsx_argmax(const void* logits_d, int dtype, int64_t rows, int64_t
   BSX_REQUIRE(row_stride >= vocab, BSX_ERR_INVALID, "row_stride smaller than vocab");
   BSX_REQUIRE(ws_bytes >= bsx_argmax_ws_bytes(rows, vocab), BSX_ERR_CAPACITY,
               "argmax workspace too small");
-  const acc::ArgmaxSplit sp = acc::argmax_split(rows, vocab);
-  float* pv = static_cast<float*>(ws_d);
-  int32_t* pc = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) + acc::align256(sp.w * sp.maxp * 4));
+  BSX_REQUIRE(dtype == BSX_DTYPE_BF16 || dtype == BSX_DTYPE_FP16 || dtype == BSX_DTYPE_FP32,
+              BSX_ERR_INVALID, "unknown dtype %d", dtype);
+  const acc::ArgmaxSplit sp = acc::argmax_split(rows, vocab, acc::elem_bytes_of(dtype));
+  BSX_REQUIRE(rows * sp.parts < (1LL << 31), BSX_ERR_UNSUPPORTED, "too many rows for one launch");
+  float* pv = reinterpret_cast<float*>(static_cast<char*>(ws_d) + argmax_values_offset());
+  int32_t* pc = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) +
+                                           argmax_columns_offset(rows, vocab));
   hipStream_t st = as_stream(stream);
-  int rc = acc::dispatch_argmax_split(logits_d, dtype, rows, vocab, row_stride, sp, pv, pc, st);
+  int rc = acc::dispatch_argmax_parts(logits_d, dtype, rows, vocab, row_stride, sp, pv, pc, st);
   if (rc != BSX_OK) return rc;
   hipLaunchKernelGGL(acc::argmax_final_kernel, dim3((unsigned)ceil_div(rows, 256)), dim3(256), 0,
-                     st, pv, pc, rows, vocab, sp.chunk, sp.maxp, out_d);
+                     st, pv, pc, rows, sp.parts, out_d);
   BSX_LAUNCH_CHECK();
   return BSX_OK;
 }
@@ -771,20 +814,23 @@ extern "C" int bsx_accept_greedy(const int64_t* draft_d, const int64_t* target_i
   const int64_t rows = (int64_t)B * (k + 1);
   float* pv = nullptr;
   int32_t* pc = nullptr;
-  acc::ArgmaxSplit sp = {0, 1, 0, 1};
+  acc::ArgmaxSplit sp = {1, 8};
   if (!target_ids_d) {
     BSX_REQUIRE(vocab > 0 && vocab < (1LL << 31), BSX_ERR_INVALID, "vocab must be in (0, 2^31)");
     BSX_REQUIRE(ws_d && ws_bytes >= bsx_accept_greedy_ws_bytes(B, k, vocab), BSX_ERR_CAPACITY,
                 "greedy workspace too small");
-    sp = acc::argmax_split(rows, vocab);
-    pv = static_cast<float*>(ws_d);
-    pc = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) + acc::align256(sp.w * sp.maxp * 4));
-    int rc = acc::dispatch_argmax_split(target_logits_d, dtype, rows, vocab, vocab, sp, pv, pc, st);
+    BSX_REQUIRE(dtype == BSX_DTYPE_BF16 || dtype == BSX_DTYPE_FP16 || dtype == BSX_DTYPE_FP32,
+                BSX_ERR_INVALID, "unknown dtype %d", dtype);
+    sp = acc::argmax_split(rows, vocab, acc::elem_bytes_of(dtype));
+    BSX_REQUIRE(rows * sp.parts < (1LL << 31), BSX_ERR_UNSUPPORTED, "too many rows for one launch");
+    pv = reinterpret_cast<float*>(static_cast<char*>(ws_d) + argmax_values_offset());
+    pc = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) + argmax_columns_offset(rows, vocab));
+    int rc = acc::dispatch_argmax_parts(target_logits_d, dtype, rows, vocab, vocab, sp, pv, pc, st);
     if (rc != BSX_OK) return rc;
   }
   hipLaunchKernelGGL(acc::greedy_eval_kernel, dim3((unsigned)ceil_div(B, 4)), dim3(256), 0, st,
-                     draft_d, target_ids_d, pv, pc, vocab, sp.chunk, sp.maxp, B, k, eos_id, mode,
-                     bonus_d, accept_d, eos_acc_d);
+                     draft_d, target_ids_d, pv, pc, sp.parts, B, k, eos_id, mode, bonus_d,
+                     accept_d, eos_acc_d);
   BSX_LAUNCH_CHECK();
   return BSX_OK;
 }

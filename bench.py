@@ -62,13 +62,17 @@ def append_bytes(b) -> int:
 
 def time_events(fn, iters: int, warmup: int):
     """Per-call durations (us) from hipEvents recorded on torch's current stream, which
-    is the stream every batchspec_amd entry point launches on."""
+    is the stream every batchspec_amd entry point launches on.  A GPU sleep is queued
+    ahead of the timed calls so the host has enqueued them all before the first one
+    runs: the events then bracket GPU time only, not the host's launch latency (which
+    a graph-captured step, as BatchSpec runs it, does not pay per call either)."""
     import torch
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    torch.cuda._sleep(50_000_000)
     for i in range(iters):
         starts[i].record()
         fn(i)

@@ -125,6 +125,24 @@ def test_greedy_posterior_ids_and_logits(rule):
             np.testing.assert_array_equal(eos_acc.cpu().numpy(), ref[2])
 
 
+def test_greedy_logits_repeated_calls_and_shapes():
+    """Back-to-back calls reusing one cached workspace across shapes agree with the
+    oracle (row counts from 6 to 3000, one to many parts per row)."""
+    say("greedy repeated calls / large batch")
+    for B, k, V in [(64, 4, 128256), (3, 1, 50), (600, 4, 1000)]:
+        c = greedy_case(B=B, k=k, V=V, seed=B + V, dtype=torch.bfloat16)
+        eos = int(c.draft_tokens[0, 0])
+        ref = OAc.greedy_posterior(c.draft_tokens.numpy(), c.target_logits.float().numpy(), eos,
+                                   "reference")
+        logits, draft = c.target_logits.to(DEV), c.draft_tokens.to(DEV)
+        for i in range(6):
+            bonus, acc, eos_acc = bsx.evaluate_posterior(draft, logits, greedy=True,
+                                                         eos_token_id=eos)
+            np.testing.assert_array_equal(bonus.cpu().numpy(), ref[0], err_msg=f"B={B} call {i}")
+            np.testing.assert_array_equal(acc.cpu().numpy(), ref[1], err_msg=f"B={B} call {i}")
+            np.testing.assert_array_equal(eos_acc.cpu().numpy(), ref[2], err_msg=f"B={B} call {i}")
+
+
 # ---------------------------------------------------------------- softmax / chain
 @pytest.mark.parametrize("dtype,V,T", [(torch.float32, 1000, 1.0), (torch.bfloat16, 128256, 1.0),
                                        (torch.bfloat16, 32000, 0.6), (torch.float16, 4099, 1.3)])
