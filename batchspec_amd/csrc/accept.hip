@@ -92,7 +92,65 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
     st[i].m = -INFINITY;
     st[i].s = 0.f;
   }
-  for (int64_t c0 = 0; (int64_t)t + 256 * c0 < G; c0 += 8) {
+  int64_t c0 = 0;
+  if (vec) {
+    // Whole rounds: the 8 groups t + 256*(c0 + i), i < 8, all exist and are complete.
+    // Their loads go out together; a new lane maximum (rare after the first rounds) is
+    // found with one ballot for the 8 lanes; then every weight, in the canonical order.
+    const int64_t G_whole = V / kGroup;
+    constexpr int VW = DT == BSX_DTYPE_FP32 ? 2 : 1;
+    for (; (int64_t)t + 256 * (c0 + 7) < G_whole; c0 += 8) {
+      u32x4 w[8][VW];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int h = 0; h < VW; ++h)
+          w[i][h] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(row) + ((int64_t)t + 256 * (c0 + i)) * VW + h);
+      float x[8][8], gm[8];
+      bool need = false;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (DT == BSX_DTYPE_FP32) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            x[i][q] = __uint_as_float(w[i][0][q]);
+            x[i][4 + q] = __uint_as_float(w[i][1][q]);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            x[i][2 * q] = lo_f32<DT>(w[i][0][q]);
+            x[i][2 * q + 1] = hi_f32<DT>(w[i][0][q]);
+          }
+        }
+        gm[i] = __builtin_elementwise_maximum(
+            __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[i][0], x[i][1]),
+                                          __builtin_elementwise_maximum(x[i][2], x[i][3])),
+            __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[i][4], x[i][5]),
+                                          __builtin_elementwise_maximum(x[i][6], x[i][7])));
+        need |= gm[i] > st[i].m;
+      }
+      if (__builtin_amdgcn_ballot_w64(need) != 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (gm[i] > st[i].m) {
+            st[i].s = st[i].s * canon::exp2(st[i].m * c - gm[i] * c);
+            st[i].m = gm[i];
+          }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float neg_rho = -(st[i].m * c);
+        // = 0 + w0 + ... exactly: weights are >= +0
+        float gs = canon::weight(x[i][0], c, neg_rho);
+#pragma unroll
+        for (int e = 1; e < 8; ++e) gs = gs + canon::weight(x[i][e], c, neg_rho);
+        st[i].s = st[i].s + gs;
+      }
+    }
+  }
+  for (; (int64_t)t + 256 * c0 < G; c0 += 8) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int64_t g = (int64_t)t + 256 * (c0 + i);
@@ -181,28 +239,28 @@ struct Chain {
   const ChainArgs& a;
   __device__ Chain(const ChainArgs& args) : a(args) {}
 
-  __device__ float2 tstat(int b, int i) const { return a.stats[(int64_t)b * (a.k + 1) + i]; }
-  __device__ float2 dstat(int b, int i) const {
+  __device__ __forceinline__ float2 tstat(int b, int i) const { return a.stats[(int64_t)b * (a.k + 1) + i]; }
+  __device__ __forceinline__ float2 dstat(int b, int i) const {
     return a.stats[(int64_t)a.B * (a.k + 1) + (int64_t)b * a.k + i];
   }
-  __device__ const void* trow(int b, int i) const {
+  __device__ __forceinline__ const void* trow(int b, int i) const {
     const size_t esz = LOGITS ? (DT == BSX_DTYPE_FP32 ? 4 : 2) : 4;
     const char* base = LOGITS ? static_cast<const char*>(a.t_logits)
                               : reinterpret_cast<const char*>(a.t_probs);
     return base + (((int64_t)b * (a.k + 1) + i) * a.V) * esz;
   }
-  __device__ const void* drow(int b, int i) const {
+  __device__ __forceinline__ const void* drow(int b, int i) const {
     const size_t esz = LOGITS ? (DT == BSX_DTYPE_FP32 ? 4 : 2) : 4;
     const char* base = LOGITS ? static_cast<const char*>(a.d_logits)
                               : reinterpret_cast<const char*>(a.d_probs);
     return base + (((int64_t)b * a.k + i) * a.V) * esz;
   }
-  __device__ bool has_draft_dist() const {
+  __device__ __forceinline__ bool has_draft_dist() const {
     return LOGITS ? a.d_logits != nullptr : a.d_probs != nullptr;
   }
 
   // p_i(v), q_i(v) as defined by the canonical order.
-  __device__ float p_at(int b, int i, int64_t v) const {
+  __device__ __forceinline__ float p_at(int b, int i, int64_t v) const {
     if constexpr (LOGITS) {
       const float2 s = tstat(b, i);
       const float x = load_one<DT>(trow(b, i), v);
@@ -211,7 +269,7 @@ struct Chain {
       return static_cast<const float*>(trow(b, i))[v];
     }
   }
-  __device__ float q_at(int b, int i, int64_t v, int64_t draft_tok) const {
+  __device__ __forceinline__ float q_at(int b, int i, int64_t v, int64_t draft_tok) const {
     if (!has_draft_dist()) return v == draft_tok ? 1.0f : 0.0f;
     if constexpr (LOGITS) {
       const float2 s = dstat(b, i);
@@ -222,90 +280,135 @@ struct Chain {
     }
   }
 
-  // Returns j (first rejected position, k if none) and the independent accept count.
-  __device__ int decide(int b, int* n_accept) const {
-    int j = a.k, cnt = 0;
-    for (int i = 0; i < a.k; ++i) {
-      const int64_t x = a.draft_ids[(int64_t)b * a.k + i];
-      bool acc = false;
-      if (x >= 0 && x < a.V) {
-        const float p = p_at(b, i, x);
-        const float q = q_at(b, i, x, x);
-        const float u = a.uniforms[(int64_t)b * (a.k + 1) + i];
-        acc = u * q < p;
-      }
-      cnt += acc ? 1 : 0;
-      if (!acc && j == a.k) j = i;
-    }
-    *n_accept = cnt;
-    return j;
+  // Ratio test of draft position i: accept iff u_i * q_i(x_i) < p_i(x_i).
+  __device__ __forceinline__ bool accepts(int b, int i) const {
+    const int64_t x = a.draft_ids[(int64_t)b * a.k + i];
+    if (x < 0 || x >= a.V) return false;
+    const float p = p_at(b, i, x);
+    const float q = q_at(b, i, x, x);
+    const float u = a.uniforms[(int64_t)b * (a.k + 1) + i];
+    return u * q < p;
   }
 
-  // Residual weights of group g of row j (j == k: target row k alone).
-  // fallback: weights of p_j (used when the residual has no mass).
-  __device__ int residual_group(int b, int j, int64_t g, bool fallback, float r[8]) const {
-    const int64_t V = a.V;
-    const int64_t x = j < a.k ? a.draft_ids[(int64_t)b * a.k + j] : -1;
-    float xt[8], xd[8];
-    const void* tr = trow(b, j);
-    const bool tvec = (((uintptr_t)tr) % 16 == 0) &&
-                      ((V * (LOGITS && DT != BSX_DTYPE_FP32 ? 2 : 4)) % 16 == 0);
-    const int n = LOGITS ? load_group<DT>(tr, g, V, tvec, xt)
-                         : load_group<BSX_DTYPE_FP32>(tr, g, V, tvec, xt);
-    const bool with_q = j < a.k && !fallback;
-    const bool dist = has_draft_dist();
-    if (with_q && dist) {
-      const void* dr = drow(b, j);
-      const bool dvec = (((uintptr_t)dr) % 16 == 0) &&
-                        ((V * (LOGITS && DT != BSX_DTYPE_FP32 ? 2 : 4)) % 16 == 0);
-      if constexpr (LOGITS) load_group<DT>(dr, g, V, dvec, xd);
-      else load_group<BSX_DTYPE_FP32>(dr, g, V, dvec, xd);
+  // j (first rejected position, k if none) and the independent accept count, for the
+  // whole workgroup: the first wave runs the k ratio tests in parallel (lane i, test i).
+  __device__ __forceinline__ int decide(int b, int* n_accept) const {
+    __shared__ int s_j, s_n;
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      int j = a.k, cnt = 0;
+      for (int i0 = 0; i0 < a.k; i0 += 64) {
+        const int i = i0 + lane;
+        const bool acc = i < a.k && accepts(b, i);
+        const uint64_t acc_bits = __builtin_amdgcn_ballot_w64(acc);
+        const uint64_t rej_bits = __builtin_amdgcn_ballot_w64(i < a.k && !acc);
+        cnt += __builtin_popcountll(acc_bits);
+        if (j == a.k && rej_bits != 0) j = i0 + __builtin_ctzll(rej_bits);
+      }
+      if (lane == 0) {
+        s_j = j;
+        s_n = cnt;
+      }
     }
-    float tnmc = 0.f, tinv = 0.f, dnmc = 0.f, dinv = 0.f;
+    __syncthreads();
+    *n_accept = s_n;
+    return s_j;
+  }
+
+  // What the residual of row j needs, computed once: row pointers, whether they can be
+  // read in 16-byte vectors, and the normalisers of p_j and q_j.
+  // (j == k: target row k alone; fallback: p_j alone, used when the residual has no
+  // mass.)
+  struct ResidualRow {
+    const void* tr;
+    const void* dr;
+    bool tvec, dvec, with_q, dist;
+    float tnmc, tinv, dnmc, dinv;
+    int64_t x;  // the draft token of row j (one-hot drafts)
+  };
+  __device__ __forceinline__ ResidualRow residual_row(int b, int j, bool fallback) const {
+    ResidualRow rr;
+    const int64_t V = a.V;
+    const int esz = LOGITS && DT != BSX_DTYPE_FP32 ? 2 : 4;
+    rr.x = j < a.k ? a.draft_ids[(int64_t)b * a.k + j] : -1;
+    rr.tr = trow(b, j);
+    rr.tvec = (((uintptr_t)rr.tr) % 16 == 0) && ((V * esz) % 16 == 0);
+    rr.with_q = j < a.k && !fallback;
+    rr.dist = has_draft_dist();
+    rr.dr = rr.with_q && rr.dist ? drow(b, j) : rr.tr;
+    rr.dvec = (((uintptr_t)rr.dr) % 16 == 0) && ((V * esz) % 16 == 0);
+    rr.tnmc = rr.tinv = rr.dnmc = rr.dinv = 0.f;
     if constexpr (LOGITS) {
       const float2 ts = tstat(b, j);
-      tnmc = -(ts.x * a.c);
-      tinv = 1.0f / ts.y;
-      if (with_q && dist) {
+      rr.tnmc = -(ts.x * a.c);
+      rr.tinv = 1.0f / ts.y;
+      if (rr.with_q && rr.dist) {
         const float2 ds = dstat(b, j);
-        dnmc = -(ds.x * a.c);
-        dinv = 1.0f / ds.y;
+        rr.dnmc = -(ds.x * a.c);
+        rr.dinv = 1.0f / ds.y;
       }
+    }
+    return rr;
+  }
+
+  // Residual weights of group g of the row prepared in rr.
+  __device__ __forceinline__ int residual_group(const ResidualRow& rr, int64_t g, float r[8]) const {
+    const int64_t V = a.V;
+    float xt[8], xd[8];
+    const int n = LOGITS ? load_group<DT>(rr.tr, g, V, rr.tvec, xt)
+                         : load_group<BSX_DTYPE_FP32>(rr.tr, g, V, rr.tvec, xt);
+    if (rr.with_q && rr.dist) {
+      if constexpr (LOGITS) load_group<DT>(rr.dr, g, V, rr.dvec, xd);
+      else load_group<BSX_DTYPE_FP32>(rr.dr, g, V, rr.dvec, xd);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float p = 0.f, q = 0.f;
       if (e < n) {
-        if constexpr (LOGITS) p = canon::weight(xt[e], a.c, tnmc) * tinv;
+        if constexpr (LOGITS) p = canon::weight(xt[e], a.c, rr.tnmc) * rr.tinv;
         else p = xt[e];
-        if (with_q) {
-          if (dist) {
-            if constexpr (LOGITS) q = canon::weight(xd[e], a.c, dnmc) * dinv;
+        if (rr.with_q) {
+          if (rr.dist) {
+            if constexpr (LOGITS) q = canon::weight(xd[e], a.c, rr.dnmc) * rr.dinv;
             else q = xd[e];
           } else {
-            q = (g * kGroup + e == x) ? 1.0f : 0.0f;
+            q = (g * kGroup + e == rr.x) ? 1.0f : 0.0f;
           }
         }
       }
-      r[e] = with_q ? fmaxf(p - q, 0.0f) : p;
+      r[e] = rr.with_q ? fmaxf(p - q, 0.0f) : p;
     }
     return n;
   }
 
-  // Lane lam = 8*tt + ii of row j: group sums (stored) and lane sum.
-  __device__ float lane_sum(int b, int j, int lam, bool fallback) const {
+  // Lane lam = 8*tt + ii of row j: group sums (stored) and lane sum.  Groups are
+  // computed NB at a time (their loads issued together), summed in canonical order.
+  __device__ __forceinline__ float lane_sum(int b, int j, int lam, bool fallback) const {
+    constexpr int NB = 4;
     const int64_t G = ceil_div(a.V, kGroup);
     const int tt = lam >> 3, ii = lam & 7;
+    const ResidualRow rr = residual_row(b, j, fallback);
     float s = 0.f;
-    for (int64_t g = (int64_t)tt + 256 * ii; g < G; g += kLanes) {
-      float r[8];
-      const int n = residual_group(b, j, g, fallback, r);
-      float gs = 0.f;
+    for (int64_t g0 = (int64_t)tt + 256 * ii; g0 < G; g0 += (int64_t)NB * kLanes) {
+      float r[NB][8];
+      int n[NB];
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (e < n) gs = gs + r[e];
-      a.gsum[(int64_t)b * G + g] = gs;
-      s = s + gs;
+      for (int u = 0; u < NB; ++u) {
+        const int64_t g = g0 + (int64_t)u * kLanes;
+        n[u] = residual_group(rr, g < G ? g : g0, r[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const int64_t g = g0 + (int64_t)u * kLanes;
+        if (g < G) {
+          float gs = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (e < n[u]) gs = gs + r[u][e];
+          a.gsum[(int64_t)b * G + g] = gs;
+          s = s + gs;
+        }
+      }
     }
     return s;
   }
@@ -392,19 +495,31 @@ __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
     float cacc = 0.f, c_at = 0.f;
     int64_t chosen = -1, last_pos = -1;
     float c_last = 0.f;
-    for (int64_t g = (int64_t)tt + 256 * ii; g < G; g += kLanes) {
-      const float gsv = gs[g];
-      const float cn = cacc + gsv;
-      if (gsv > 0.f) {
-        last_pos = g;
-        c_last = cacc;
+    // the lane's group sums, 16 loaded together, scanned in order
+    constexpr int NB = 16;
+    for (int64_t g0 = (int64_t)tt + 256 * ii; g0 < G && chosen < 0; g0 += (int64_t)NB * kLanes) {
+      float v[NB];
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const int64_t g = g0 + (int64_t)u * kLanes;
+        v[u] = gs[g < G ? g : g0];
       }
-      if (tg < cn) {
-        chosen = g;
-        c_at = cacc;
-        break;
+      for (int u = 0; u < NB; ++u) {
+        const int64_t g = g0 + (int64_t)u * kLanes;
+        if (g >= G) break;
+        const float gsv = v[u];
+        const float cn = cacc + gsv;
+        if (gsv > 0.f) {
+          last_pos = g;
+          c_last = cacc;
+        }
+        if (tg < cn) {
+          chosen = g;
+          c_at = cacc;
+          break;
+        }
+        cacc = cn;
       }
-      cacc = cn;
     }
     if (chosen < 0) {
       chosen = last_pos;
@@ -414,7 +529,7 @@ __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
     if (chosen >= 0) {
       const float tl = tg - c_at;
       float r[8];
-      const int n = ch.residual_group(b, j, chosen, fallback, r);
+      const int n = ch.residual_group(ch.residual_row(b, j, fallback), chosen, r);
       float s = 0.f;
       int64_t last_e = -1;
       for (int e = 0; e < n; ++e) {

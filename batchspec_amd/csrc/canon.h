@@ -3,9 +3,11 @@
 // Acceptance must give bit-identical token ids on the GPU and on a CPU restatement
 // fed the same uniforms.  That requires every floating-point value the decisions
 // depend on to be produced by the same sequence of IEEE-754 binary32 operations:
-//   * exp is our own: 2^y = 2^n * P(f), n = rint(y), f = y - n in [-1/2, 1/2], P the
-//     degree-6 Taylor polynomial of 2^f (coefficients ln2^k/k! rounded to binary32),
-//     evaluated by Horner with fused multiply-add; max relative error 1.6e-7.
+//   * exp is our own: 2^y = 2^n * P(f), n = floor(y), f = fl(y - n) capped at the
+//     largest float below 1 (the GPU's v_fract_f32 and v_cvt_flr_i32_f32), P a
+//     degree-5 polynomial with P(0) = 1 fitted to 2^f on [0, 1) for relative error
+//     (Lawson iteration, coefficients rounded to binary32 and tuned in the last bit),
+//     evaluated by Horner with fused multiply-add; at most 3 ulp from 2^y.
 //     Arguments below -200 are clamped (2^-200 underflows to 0 in ldexp).
 //   * every sum runs over a fixed tree, independent of the launch configuration:
 //       - a row of V values is cut into groups of 8 consecutive elements
@@ -46,25 +48,30 @@ constexpr int kLaneStride = kLanes;                  // groups between consecuti
 
 constexpr float kLog2e = 0x1.715476p+0f;
 constexpr float kC0 = 0x1.0p+0f;
-constexpr float kC1 = 0x1.62e430p-1f;
-constexpr float kC2 = 0x1.ebfbe0p-3f;
-constexpr float kC3 = 0x1.c6b08ep-5f;
-constexpr float kC4 = 0x1.3b2ab6p-7f;
-constexpr float kC5 = 0x1.5d87fep-10f;
-constexpr float kC6 = 0x1.430912p-13f;
+constexpr float kC1 = 0x1.62e4bap-1f;
+constexpr float kC2 = 0x1.ebdb5ap-3f;
+constexpr float kC3 = 0x1.c91ce4p-5f;
+constexpr float kC4 = 0x1.277854p-7f;
+constexpr float kC5 = 0x1.e974f6p-10f;
 
 BSX_HD float exp2(float y) {
   y = fmaxf(y, -200.0f);
-  float n = rintf(y);
-  float f = y - n;
-  float p = kC6;
-  p = fmaf(p, f, kC5);
+#ifdef __HIP_DEVICE_COMPILE__
+  const float f = __builtin_amdgcn_fractf(y);
+  int n;
+  asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(n) : "v"(y));
+#else
+  const float fl = floorf(y);
+  const float f = fminf(y - fl, 0x1.fffffep-1f);
+  const int n = (int)fl;
+#endif
+  float p = kC5;
   p = fmaf(p, f, kC4);
   p = fmaf(p, f, kC3);
   p = fmaf(p, f, kC2);
   p = fmaf(p, f, kC1);
   p = fmaf(p, f, kC0);
-  return ldexpf(p, (int)n);
+  return ldexpf(p, n);
 }
 
 // Scale C = log2(e) / T.

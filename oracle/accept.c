@@ -14,8 +14,10 @@
  *
  * Floating-point values follow the deterministic ("canonical") order the GPU kernels
  * document, restated here from that specification:
- *   exp2(y): y = max(y, -200); n = rint(y); f = y - n; P(f) = Horner-fma of the
- *            degree-6 Taylor polynomial of 2^f (ln2^k/k! in binary32); ldexp(P, n).
+ *   exp2(y): y = max(y, -200); n = floor(y); f = min(fl(y - n), largest float < 1);
+ *            P(f) = Horner-fma of the degree-5 polynomial with P(0) = 1 fitted to
+ *            2^f on [0, 1) for relative error (binary32 coefficients below);
+ *            ldexp(P, n).
  *   weights: w(x) = exp2(fma(x, C, -(M*C))), C = log2(e) * (1/T).
  *   groups of 8 consecutive elements; lane (8t+i) owns groups t + 256*i + 2048*j.
  *   row stats: per lane, running max m with reference fl(m*C) (rescale on a new max),
@@ -34,16 +36,17 @@
 #define NL 2048
 
 static const float LOG2E = 0x1.715476p+0f;
-static const float TAY[7] = {0x1.0p+0f,      0x1.62e430p-1f, 0x1.ebfbe0p-3f, 0x1.c6b08ep-5f,
-                             0x1.3b2ab6p-7f, 0x1.5d87fep-10f, 0x1.430912p-13f};
+static const float POLY[6] = {0x1.0p+0f,      0x1.62e4bap-1f, 0x1.ebdb5ap-3f,
+                              0x1.c91ce4p-5f, 0x1.277854p-7f, 0x1.e974f6p-10f};
 
 float oc_exp2(float y) {
   if (y < -200.0f || y != y) y = -200.0f; /* fmaxf(y, -200): NaN -> -200 */
-  float n = rintf(y);
-  float f = y - n;
-  float p = TAY[6];
-  for (int i = 5; i >= 0; --i) p = fmaf(p, f, TAY[i]);
-  return ldexpf(p, (int)n);
+  float fl = floorf(y);
+  float f = y - fl;
+  if (f > 0x1.fffffep-1f) f = 0x1.fffffep-1f; /* fract is below 1 */
+  float p = POLY[5];
+  for (int i = 4; i >= 0; --i) p = fmaf(p, f, POLY[i]);
+  return ldexpf(p, (int)fl);
 }
 
 static float weight(float x, float c, float neg_mc) { return oc_exp2(fmaf(x, c, neg_mc)); }

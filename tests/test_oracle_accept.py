@@ -11,7 +11,8 @@ from oracle import accept as A
 
 # ---------------------------------------------------------------- exp2 / softmax
 def test_exp2_within_three_ulp_of_libm(oracle_lib):
-    ys = np.concatenate([np.linspace(-125.0, 0.0, 50001, dtype=np.float32),
+    # the polynomial's worst case on [0, 1) is 2.13 ulp, plus the rounding of y - floor(y)
+    ys = np.concatenate([np.linspace(-125.0, 0.0, 500001, dtype=np.float32),
                          np.float32(-np.random.default_rng(0).random(20000) * 30)])
     got = A.exp2_array(ys).astype(np.float64)
     ref = np.exp2(ys.astype(np.float64))
