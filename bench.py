@@ -94,6 +94,64 @@ def measured_traffic():
     return int(m.group(1)) if m else None
 
 
+def extra_configs(dev, iters: int):
+    """Verify attention at configs 4 (EAGLE tree), 3b (long context, split-KV) and 3a
+    (the MagicDec draft over a 64-sink + 512-window view), each over rotating input sets
+    (one for 3b: 6.4 GB of KV), timed like the headline pass."""
+    import numpy as np
+    import torch
+    import batchspec_amd as bsx
+    from batchspec_amd.workloads import config3, config4, make_verify_batch
+
+    def run(name, sets, plan_kw, nbytes, n):
+        ws = [torch.empty(512 << 20, dtype=torch.uint8, device=dev) for _ in sets]
+        wr = []
+        for b, w_buf in zip(sets, ws):
+            w = bsx.BatchPrefillWithPagedKVCacheWrapper(w_buf, "NHD")
+            kw = dict(plan_kw)
+            if kw.pop("tree", False):
+                kw["tree_mask_words"] = b.mask_words
+            w.plan(b.qo_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, b.num_qo_heads,
+                   b.num_kv_heads, b.head_dim, b.page_size, q_data_type=torch.bfloat16, **kw)
+            wr.append(w)
+        outs = [torch.empty_like(b.q) for b in sets]
+        k = len(sets)
+        us = time_events(lambda i: wr[i % k].run(sets[i % k].q, sets[i % k].cache, out=outs[i % k]),
+                         n, 3)
+        t = sum(us) / len(us)
+        nb = sum(nbytes) / k
+        p = wr[0].plan_info
+        return {"us": round(t, 2), "GB/s": round(nb / t / 1e3, 1),
+                "frac": round(nb / t / 1e3 / HBM_PEAK_GBS, 4), "bytes": int(nb),
+                "plan": {"workgroups": int(p.num_ctas), "segments": int(p.num_segments),
+                         "split_requests": int(p.num_split_requests),
+                         "shared_kv_tiles": int(p.shared_kv_tiles),
+                         "heads_per_workgroup": int(p.heads_per_cta),
+                         "waves_per_head": int(p.qblocks_per_cta)}}
+
+    out = {}
+    s4 = [config4(device=dev, seed=1004 + i) for i in range(3)]
+    out["config4_tree_attention"] = run("4", s4, dict(causal=False, tree=True),
+                                        [attn_bytes(b) for b in s4], iters)
+    del s4
+    s3 = [config3(device=dev, seed=1003)]
+    out["config3b_verify_attention"] = run("3b", s3, dict(causal=True), [attn_bytes(s3[0])],
+                                           max(5, iters // 3))
+    del s3
+    s3a = [make_verify_batch(32, 32768, 65536, 1, 32, 8, 128, 16, dtype=torch.bfloat16,
+                             scale=0.5, seed=1003 + i, device=dev) for i in range(2)]
+
+    def view_bytes(b):  # K/V rows of the 64 + 512 view, Q, O, page ids of the view
+        view = int(np.sum(np.minimum(b.kv_lens, 576)))
+        return (view * b.num_kv_heads * b.head_dim * 4 + 2 * b.q.numel() * 2
+                + int(np.sum(np.minimum(np.diff(b.kv_indptr.cpu().numpy()), 36 + 1))) * 4)
+    out["config3a_draft_attention"] = run("3a", s3a, dict(causal=True, sink_tokens=64,
+                                                          window_tokens=512),
+                                          [view_bytes(b) for b in s3a], iters)
+    del s3a
+    return out
+
+
 def cpu_baseline(sets, budget_s: float = 12.0):
     """fp32 oracle (numpy paged gather + softmax attention) over the config-2 requests,
     cycling through the batch until about budget_s of CPU work; reported in the
@@ -159,6 +217,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-accept", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--extra-configs", action="store_true",
+                    help="also time verify attention at configs 4, 3b and 3a")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the "
@@ -309,6 +369,10 @@ def main() -> int:
                                        "frac": round(sbytes / t_st / 1e3 / HBM_PEAK_GBS, 4),
                                        "bytes": sbytes}
         del s
+
+    if args.extra_configs:
+        print("bench: configs 4, 3b, 3a", file=sys.stderr, flush=True)
+        result.update(extra_configs(dev, args.steps))
 
     if not args.no_cpu_baseline:
         print("bench: CPU baseline (fp32 oracle, ~12 s)", file=sys.stderr, flush=True)
