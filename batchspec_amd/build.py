@@ -26,7 +26,8 @@ ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are kept off for all device code.  The acceptance and
 # softmax translation unit also forbids implicit multiply-add contraction: its
-# floating-point operation sequence is part of its bit-exact contract.
+# floating-point operation sequence is part of its bit-exact contract (as is the
+# sampling filter's).
 HIP_COMMON = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -38,6 +39,7 @@ HIP_SOURCES = {
     "append.hip": [],
     "collate.hip": [],
     "accept.hip": ["-ffp-contract=off"],
+    "filter.hip": ["-ffp-contract=off"],
 }
 CXX_SOURCES = ["abi.cpp", "plan.cpp"]
 

@@ -106,5 +106,35 @@ BSX_HD float lane_rescaled(LaneState st, float c, float rho_m) {
   return st.s * exp2(st.m * c - rho_m);
 }
 
+// ---- top-k / top-p filtering and fixed-point draws ----------------------------
+// Order-preserving 32-bit image of a finite float (-0 maps like +0).
+BSX_HD uint32_t okey(float x) {
+  uint32_t b = __builtin_bit_cast(uint32_t, x);
+  if (b == 0x80000000u) b = 0u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+BSX_HD float key_value(uint32_t k) {
+  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+// Fixed-point mass of a weight: trunc(w * 2^40) (w * 2^40 is exact).
+BSX_HD uint64_t fx40(float w) { return w > 0.0f ? (uint64_t)(w * 0x1p40f) : 0ull; }
+// Round-to-nearest-even conversion of a 64-bit integer to binary32.
+BSX_HD float u64_to_f32(uint64_t v) {
+  if (v < (1ull << 24)) return (float)(uint32_t)v;
+  const int n = 64 - __builtin_clzll(v);
+  const int sh = n - 24;
+  uint64_t mant = v >> sh;
+  const uint64_t rem = v & ((1ull << sh) - 1);
+  const uint64_t half = 1ull << (sh - 1);
+  if (rem > half || (rem == half && (mant & 1))) ++mant;
+  return ldexpf((float)(uint32_t)mant, sh);
+}
+// Draw point of a uniform over a fixed-point total: floor(u * total) in binary64
+// (0 for u <= 0 or NaN).
+BSX_HD uint64_t draw_point(float u, uint64_t total) {
+  if (!(u > 0.0f)) return 0ull;
+  return (uint64_t)floor((double)u * (double)total);
+}
+
 }  // namespace canon
 }  // namespace bsx

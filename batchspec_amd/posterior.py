@@ -8,7 +8,8 @@ Same inputs and outputs as MTPEngine.evaluate_posterior
   returns (bonus [B,1] int64, accept_nums [B] int64, eos_accepted [B,1] bool) with
   the reference rule accept = (#positions where draft == target)+1
   (mtp_engine.py:556).  ``accept_rule="prefix"`` selects the longest-prefix rule.
-* sampling (``target_preds`` = logits [B, k+1, V]): softmax at the temperature,
+* sampling (``target_preds`` = logits [B, k+1, V]): softmax at the temperature with
+  the top-p / top-k renormalisation of get_sampling_probs (mtp_engine.py:564),
   one-hot draft probabilities, chain speculative sampling; returns
   (bonus [B,1] int32, accept_nums = emitted+1 [B] int32, eos_accepted [B,1] bool),
   the dtypes of the reference's FlashInfer branch.
@@ -36,12 +37,11 @@ def evaluate_posterior(draft_tokens: torch.Tensor, target_preds: torch.Tensor, *
     B, k = draft_tokens.shape
     if greedy:
         return _greedy(draft_tokens, target_preds, eos_token_id, _RULES[accept_rule])
-    if (0 < top_p < 1.0) or top_k > 0:
-        raise NotImplementedError("top-p / top-k renormalisation is not implemented")
     if target_preds.dim() != 3:
         raise ValueError("sampling acceptance needs target logits [B, k+1, V]")
     out, _, emitted = chain_speculative_sampling_from_logits(
-        None, draft_tokens, target_preds, temperature, generator, uniforms=uniforms)
+        None, draft_tokens, target_preds, temperature, generator, uniforms=uniforms,
+        top_k=top_k, top_p=top_p)
     accept_nums = emitted + 1
     last = (out != -1).to(torch.long) * torch.arange(out.shape[1], device=out.device)
     bonus = out.gather(1, last.argmax(dim=1, keepdim=True))

@@ -10,9 +10,14 @@
   temperature softmax of both distributions (reads bf16 logits once).
 * ``softmax`` — flashinfer.sampling.softmax as used at
   batchspec/backends/utils/sampling.py:48.
-* ``argmax`` / ``sample`` (greedy) — batchspec/backends/utils/sampling.py:89-90.
-* ``get_sampling_probs`` — batchspec/backends/utils/sampling.py:18-58 for
-  top-p = 1 (or <= 0) and top-k <= 0.
+* ``argmax`` — batchspec/backends/utils/sampling.py:89-90 (greedy ``sample``).
+* ``get_sampling_probs`` — batchspec/backends/utils/sampling.py:18-58: softmax at the
+  temperature, then top-p renormalisation (top_p > 0), then top-k (top_k > 0).
+* ``sample`` — batchspec/backends/utils/sampling.py:61-115 with an explicit uniform
+  per row (greedy at temperature 0).
+Top-k / top-p keep every value at or above a threshold (ties kept): top-p on the full
+distribution, then top-k on the renormalised one (the reference's order); top-p >= 1
+and top-k >= vocab keep everything.
 """
 from __future__ import annotations
 
@@ -94,11 +99,14 @@ def chain_speculative_sampling_from_logits(draft_logits: Optional[torch.Tensor],
                                            draft_token_ids: torch.Tensor,
                                            target_logits: torch.Tensor, temperature: float = 1.0,
                                            generator: Optional[torch.Generator] = None, *,
-                                           uniforms: Optional[torch.Tensor] = None
+                                           uniforms: Optional[torch.Tensor] = None,
+                                           top_k: int = 0, top_p: float = 1.0
                                            ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """``chain_speculative_sampling(softmax(draft/T), ids, softmax(target/T))`` in one pass
-    over bf16/fp16/fp32 logits; draft_logits None means one-hot draft probabilities
-    (the MTP case, batchspec/backends/mtp_engine.py:565-567)."""
+    """``chain_speculative_sampling(get_sampling_probs(draft), ids,
+    get_sampling_probs(target))`` over bf16/fp16/fp32 logits without materialising
+    probabilities; draft_logits None means one-hot draft probabilities (the MTP case,
+    batchspec/backends/mtp_engine.py:565-567).  top_k / top_p filter both
+    distributions (sampling.py:50-56)."""
     dev = require_gpu("chain_speculative_sampling_from_logits", draft_token_ids, target_logits,
                       draft_logits)
     B, k = draft_token_ids.shape
@@ -116,13 +124,13 @@ def chain_speculative_sampling_from_logits(draft_logits: Optional[torch.Tensor],
     acc = torch.empty(B, dtype=torch.int32, device=dev)
     emi = torch.empty(B, dtype=torch.int32, device=dev)
     lib = _lib.load()
-    ws = _ws(dev, int(lib.bsx_chain_ws_bytes(B, k, V)), "chain")
+    ws = _ws(dev, int(lib.bsx_chain_filtered_ws_bytes(B, k, V)), "chain")
     tl = target_logits.contiguous()
     dl = None if draft_logits is None else draft_logits.contiguous()
-    rc = lib.bsx_chain_speculative_sampling_logits(
+    rc = lib.bsx_chain_speculative_sampling_filtered(
         _lib.ptr(dl), ids.data_ptr(), tl.data_ptr(), dtype_code(tl.dtype), float(temperature),
-        u.data_ptr(), B, k, V, out.data_ptr(), acc.data_ptr(), emi.data_ptr(), ws.data_ptr(),
-        ws.numel(), stream_of(dev))
+        int(top_k), float(top_p), u.data_ptr(), B, k, V, out.data_ptr(), acc.data_ptr(),
+        emi.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(dev))
     _lib.check(rc, "chain_speculative_sampling_from_logits")
     return out, acc, emi
 
@@ -172,17 +180,49 @@ def _flatten(logits: torch.Tensor) -> Tuple[torch.Tensor, int, int]:
 
 def get_sampling_probs(logits: torch.Tensor, top_p: float, top_k: int,
                        temperature: float) -> torch.Tensor:
-    """Probabilities [B, S, V] = softmax(logits / T); top-p / top-k renormalisation
-    (sampling.py:50-56) is not implemented yet and raises."""
+    """Probabilities [B, S, V] (fp32) of softmax(logits / T) after the top-p and top-k
+    renormalisation of sampling.py:50-56."""
     flat, B, S = _flatten(logits)
-    if (0 < top_p < 1.0) or top_k > 0:
-        raise NotImplementedError("top-p / top-k renormalisation is not implemented")
-    return softmax(flat, temperature).reshape(B, S, flat.shape[-1])
+    dev = require_gpu("get_sampling_probs", flat)
+    if not temperature > 0:
+        raise ValueError("temperature must be > 0")
+    x = flat.contiguous()
+    rows, V = x.shape
+    probs = torch.empty((rows, V), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws = _ws(dev, int(lib.bsx_sampling_probs_ws_bytes(rows)), "probs")
+    rc = lib.bsx_sampling_probs(x.data_ptr(), dtype_code(x.dtype), float(temperature), int(top_k),
+                                float(top_p), rows, V, probs.data_ptr(), ws.data_ptr(), ws.numel(),
+                                stream_of(dev))
+    _lib.check(rc, "get_sampling_probs")
+    return probs.reshape(B, S, V)
 
 
-def sample(logits: torch.Tensor, top_p: float, top_k: int, temperature: float) -> torch.Tensor:
-    """Greedy (temperature 0) token choice [B, S] int64 (sampling.py:61-90)."""
+def sample(logits: torch.Tensor, top_p: float, top_k: int, temperature: float, *,
+           uniforms: Optional[torch.Tensor] = None,
+           generator: Optional[torch.Generator] = None) -> torch.Tensor:
+    """Token ids [B, S] int64 (sampling.py:61-115): argmax at temperature 0, else one draw
+    per row from the filtered distribution driven by ``uniforms`` [B*S] (or [B, S])
+    fp32 in [0, 1) (drawn from ``generator`` when not given)."""
     flat, B, S = _flatten(logits)
     if temperature == 0:
         return argmax(flat).reshape(B, S)
-    raise NotImplementedError("non-greedy sample() is not implemented; use the acceptance kernels")
+    dev = require_gpu("sample", flat)
+    if not temperature > 0:
+        raise ValueError("temperature must be >= 0")
+    x = flat.contiguous()
+    rows, V = x.shape
+    if uniforms is None:
+        u = torch.rand(rows, dtype=torch.float32, device=dev, generator=generator)
+    else:
+        if uniforms.numel() != rows or uniforms.dtype != torch.float32:
+            raise ValueError(f"uniforms must be float32 with {rows} elements")
+        u = uniforms.reshape(rows).contiguous()
+    ids = torch.empty(rows, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    ws = _ws(dev, int(lib.bsx_sample_ws_bytes(rows, V)), "sample")
+    rc = lib.bsx_sample(x.data_ptr(), dtype_code(x.dtype), float(temperature), int(top_k),
+                        float(top_p), u.data_ptr(), rows, V, ids.data_ptr(), ws.data_ptr(),
+                        ws.numel(), stream_of(dev))
+    _lib.check(rc, "sample")
+    return ids.reshape(B, S).long()

@@ -264,6 +264,43 @@ int bsx_softmax(const void* logits_d, int dtype, float temperature, int64_t rows
                 int64_t vocab, float* probs_d, void* ws_d, int64_t ws_bytes,
                 void* stream);
 
+/* Top-k / top-p renormalisation (batchspec/backends/utils/sampling.py:50-56: top-p on
+ * the full softmax(logits/T), then top-k on the renormalised distribution; top-k is on
+ * iff 0 < top_k < vocab, top-p iff 0 < top_p < 1) fused into the stochastic acceptance
+ * (mtp_engine.py:561-575 with get_sampling_probs(target_preds, top_p, top_k, T) at
+ * :564).  The kept set is every value at or above a threshold (ties kept); threshold
+ * masses and draws use 2^-40 fixed point, so the ids are bit-identical to the CPU
+ * restatement given the same uniforms.  draft_logits_d (or NULL: one-hot draft) is
+ * filtered the same way.  With both filters off this is
+ * bsx_chain_speculative_sampling_logits.  ws_d: bsx_chain_filtered_ws_bytes. */
+int64_t bsx_filter_ws_bytes(int64_t rows);
+int64_t bsx_chain_filtered_ws_bytes(int B, int k, int64_t vocab);
+int bsx_chain_speculative_sampling_filtered(const void* draft_logits_d,
+                                            const int64_t* draft_ids_d,
+                                            const void* target_logits_d, int dtype,
+                                            float temperature, int top_k, float top_p,
+                                            const float* uniforms_d, int B, int k,
+                                            int64_t vocab, int32_t* out_ids_d,
+                                            int32_t* accepted_d, int32_t* emitted_d,
+                                            void* ws_d, int64_t ws_bytes, void* stream);
+
+/* get_sampling_probs (batchspec/backends/utils/sampling.py:18-58): fp32 probabilities
+ * [rows, vocab] of softmax(logits/T) after the top-p and top-k renormalisation above
+ * (bsx_softmax when both are off).  ws_d: bsx_sampling_probs_ws_bytes. */
+int64_t bsx_sampling_probs_ws_bytes(int64_t rows);
+int bsx_sampling_probs(const void* logits_d, int dtype, float temperature, int top_k,
+                       float top_p, int64_t rows, int64_t vocab, float* probs_d, void* ws_d,
+                       int64_t ws_bytes, void* stream);
+
+/* sample() (batchspec/backends/utils/sampling.py:61-115) for temperature > 0: one id
+ * per row of [rows, vocab] logits drawn from the filtered distribution with
+ * uniforms_d[row] (int32 ids, as FlashInfer's samplers return before the reference's
+ * .long() at :114).  Temperature 0 is bsx_argmax.  ws_d: bsx_sample_ws_bytes. */
+int64_t bsx_sample_ws_bytes(int64_t rows, int64_t vocab);
+int bsx_sample(const void* logits_d, int dtype, float temperature, int top_k, float top_p,
+               const float* uniforms_d, int64_t rows, int64_t vocab, int32_t* out_d,
+               void* ws_d, int64_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,6 +6,9 @@
 * ``chain_probs`` / ``chain_logits`` / ``softmax`` / ``tree_draw`` / ``exp2`` — the
   canonical stochastic acceptance of accept.c (ctypes), which restates
   mtp_engine.py:561-575 and batchspec/backends/utils/sampling.py:18-58.
+* ``filter_row`` / ``filtered_probs`` / ``chain_filtered`` / ``sample`` / ``fx_draw`` —
+  the top-k / top-p renormalisation (sampling.py:50-56), non-greedy sample()
+  (sampling.py:61-115) and the acceptance fed filtered distributions, from filter.c.
 """
 from __future__ import annotations
 
@@ -36,6 +39,20 @@ def lib() -> ctypes.CDLL:
                                      c_void_p, c_void_p, c_void_p]
         L.oc_chain_logits.argtypes = [c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_int, c_int,
                                       c_int64, c_void_p, c_void_p, c_void_p]
+        L.oc_okey.restype = ctypes.c_uint32
+        L.oc_okey.argtypes = [c_float]
+        L.oc_u64_to_f32.restype = c_float
+        L.oc_u64_to_f32.argtypes = [ctypes.c_uint64]
+        L.oc_filter_row.argtypes = [c_void_p, c_int64, c_float, c_int, c_float, c_void_p, c_void_p,
+                                    c_void_p, c_void_p]
+        L.oc_fx_draw.restype = c_int64
+        L.oc_fx_draw.argtypes = [c_void_p, c_int64, c_float]
+        L.oc_filtered_probs.argtypes = [c_void_p, c_int64, c_int64, c_float, c_int, c_float, c_void_p]
+        L.oc_chain_filtered.argtypes = [c_void_p, c_void_p, c_void_p, c_float, c_int, c_float,
+                                        c_void_p, c_int, c_int, c_int64, c_void_p, c_void_p,
+                                        c_void_p]
+        L.oc_sample.argtypes = [c_void_p, c_int64, c_int64, c_float, c_int, c_float, c_void_p,
+                                c_void_p]
         _lib = L
     return _lib
 
@@ -134,3 +151,69 @@ def greedy_posterior(draft_tokens, target_preds, eos_token_id: int, rule: str = 
     bonus = preds[np.arange(B), accept - 1]
     eos = ((draft == eos_token_id) & counted).any(axis=1)
     return bonus[:, None], accept.astype(np.int64), eos[:, None]
+
+
+def okey(x: float) -> int:
+    return int(lib().oc_okey(float(np.float32(x))))
+
+
+def u64_to_f32(v: int) -> float:
+    return float(lib().oc_u64_to_f32(int(v)))
+
+
+def filter_row(row, temperature: float, top_k: int, top_p: float):
+    """-> (M, inv_k, t_key, zk_fx) of one row (the filtered distribution's parameters)."""
+    x = _f32(row)
+    M = np.zeros(1, np.float32)
+    inv = np.zeros(1, np.float32)
+    t = np.zeros(1, np.uint32)
+    zk = np.zeros(1, np.uint64)
+    lib().oc_filter_row(x.ctypes.data, x.size, float(temperature), int(top_k), float(top_p),
+                        M.ctypes.data, inv.ctypes.data, t.ctypes.data, zk.ctypes.data)
+    return float(M[0]), float(inv[0]), int(t[0]), int(zk[0])
+
+
+def fx_draw(weights, u: float) -> int:
+    w = _f32(weights)
+    return int(lib().oc_fx_draw(w.ctypes.data, w.size, float(np.float32(u))))
+
+
+def filtered_probs(logits, temperature: float, top_k: int, top_p: float) -> np.ndarray:
+    x = _f32(logits)
+    V = x.shape[-1]
+    out = np.empty_like(x)
+    lib().oc_filtered_probs(x.ctypes.data, x.size // V, V, float(temperature), int(top_k),
+                            float(top_p), out.ctypes.data)
+    return out
+
+
+def chain_filtered(draft_logits, draft_ids, target_logits, temperature, top_k, top_p, uniforms):
+    """Chain acceptance over top-k / top-p filtered softmax distributions."""
+    ids = np.ascontiguousarray(np.asarray(draft_ids, dtype=np.int64))
+    B, k = ids.shape
+    tl = _f32(target_logits)
+    V = tl.shape[-1]
+    dl = None if draft_logits is None else _f32(draft_logits)
+    u = _f32(uniforms)
+    out = np.empty((B, k + 1), np.int32)
+    acc = np.empty(B, np.int32)
+    emi = np.empty(B, np.int32)
+    lib().oc_chain_filtered(None if dl is None else dl.ctypes.data, ids.ctypes.data,
+                            tl.ctypes.data, float(temperature), int(top_k), float(top_p),
+                            u.ctypes.data, B, k, V, out.ctypes.data, acc.ctypes.data,
+                            emi.ctypes.data)
+    return out, acc, emi
+
+
+def sample(logits, temperature: float, top_k: int, top_p: float, uniforms) -> np.ndarray:
+    """sample() for temperature > 0: one draw per row of [rows, V] with uniforms[rows]."""
+    x = _f32(logits)
+    V = x.shape[-1]
+    rows = x.size // V
+    u = _f32(uniforms).reshape(-1)
+    if u.size != rows:
+        raise ValueError("one uniform per row")
+    out = np.empty(rows, np.int64)
+    lib().oc_sample(x.ctypes.data, rows, V, float(temperature), int(top_k), float(top_p),
+                    u.ctypes.data, out.ctypes.data)
+    return out

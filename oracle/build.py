@@ -1,5 +1,5 @@
-"""ORACLE — TEST INFRASTRUCTURE ONLY.  Builds oracle/liboracle.so from accept.c with
-gcc (strict IEEE binary32: no fast-math, no implicit multiply-add contraction)."""
+"""ORACLE — TEST INFRASTRUCTURE ONLY.  Builds oracle/liboracle.so from accept.c and
+filter.c with gcc (strict IEEE binary32: no fast-math, no implicit multiply-add contraction)."""
 from __future__ import annotations
 
 import subprocess
@@ -12,7 +12,7 @@ SO = HERE / "liboracle.so"
 def build() -> Path:
     tmp = SO.with_suffix(".so.tmp")
     subprocess.run(["gcc", "-O2", "-std=c11", "-ffp-contract=off", "-fno-fast-math", "-fPIC",
-                    "-shared", "-o", str(tmp), str(HERE / "accept.c"), "-lm"], check=True)
+                    "-shared", "-o", str(tmp), str(HERE / "accept.c"), str(HERE / "filter.c"), "-lm"], check=True)
     tmp.replace(SO)
     return SO
 
