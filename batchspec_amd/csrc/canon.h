@@ -116,8 +116,16 @@ BSX_HD uint32_t okey(float x) {
 BSX_HD float key_value(uint32_t k) {
   return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
-// Fixed-point mass of a weight: trunc(w * 2^40) (w * 2^40 is exact).
-BSX_HD uint64_t fx40(float w) { return w > 0.0f ? (uint64_t)(w * 0x1p40f) : 0ull; }
+// Fixed-point mass of a weight: trunc(w * 2^40) (w * 2^40 is exact), 0 unless w > 0,
+// read off the bits (finite w below 2^23).
+BSX_HD uint64_t fx40(float w) {
+  if (!(w > 0.0f)) return 0ull;
+  const uint32_t b = __builtin_bit_cast(uint32_t, w * 0x1p40f);
+  const int e = (int)(b >> 23) - 150;  // value = mant * 2^e
+  const uint64_t mant = (uint64_t)((b & 0x7fffffu) | 0x800000u);
+  if ((b >> 23) == 0u) return 0ull;    // below 1
+  return e >= 0 ? mant << e : (e > -24 ? mant >> -e : 0ull);
+}
 // Round-to-nearest-even conversion of a 64-bit integer to binary32.
 BSX_HD float u64_to_f32(uint64_t v) {
   if (v < (1ull << 24)) return (float)(uint32_t)v;

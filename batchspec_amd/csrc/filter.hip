@@ -30,21 +30,21 @@
 //
 // Kernels:
 //   filter_rows_kernel: one 256-thread workgroup per row.
-//     1. canonical (M, Z), keeping the 2048 lane maxima;
-//     2. a lower bound L of t*: the k-th largest lane maximum is at most the k-th
-//        largest element, so the lower edge of its 12-bit key bin bounds t* from
-//        below (for top-p alone the bound of rank 64 is used and checked afterwards);
-//     3. the row is read again (the first pass left it in the memory-side cache) and
-//        the elements >= L are listed in LDS;
-//     4. with at most kCap of them, every listed element gets its count and mass of
-//        listed elements at or above it (all of the row's elements there are listed),
-//        which gives t* and Z_K exactly; the kept elements are written out;
-//     5. otherwise (ties, a large k, a wide nucleus), an exact radix select over the
-//        key bits, 8 per pass, with counts and fixed-point masses per digit in LDS,
-//        and the row gets no list.
+//     1. the canonical (M, Z) pass lists candidates on the way: the k-th largest of
+//        the maxima of 2048 disjoint groups (read first) bounds t* from below; groups
+//        are listed only when their maximum reaches it (for top-p alone the bound of
+//        rank 64 is used);
+//     2. with at most kCands candidates, each gets the count and mass of the listed
+//        keys at or above its own (every element of the row there is listed), which
+//        gives t* and Z_K exactly, and the kept indices are written out;
+//     3. if the list overflowed (or the row is too short for step 1), the bound of all
+//        2048 lane maxima and a second read of the row list the candidates again;
+//     4. if that fails too (ties, a large k, a nucleus below the bound), an exact radix
+//        select over the key bits, 8 per pass, with counts and fixed-point masses per
+//        digit in LDS; the row then gets no list.
 //   filter_chain_kernel: one workgroup per request: the ratio tests, then the draw
 //     from the row the chain stops at, over its kept list, or over the whole row in
-//     contiguous chunks when it has none.
+//     wave-sized tiles (tile sums, their prefix, the lane, the element) without one.
 //   filtered_probs_kernel: p'(x) for every element (get_sampling_probs).
 #include <limits.h>
 
@@ -60,16 +60,22 @@ namespace filt {
 
 using acc::load_one;
 using canon::fx40;
+using canon::kGroup;
 using canon::key_value;
 using canon::okey;
 
 constexpr int kThreads = 256;
-constexpr int kCap = 256;         // listed candidates per row (fast path)
+constexpr int kCands = 1024;      // candidates listed in LDS per row
+constexpr int kCap = 256;         // kept elements listed per row for the draw
 constexpr int kTopPProbe = 64;    // rank of the lane-maximum bound for top-p alone
-constexpr int kBinShift = 20;     // 12-bit key bins for the bound
+constexpr int kMaxTiles = 2048;   // tiles of a whole-row draw
+constexpr int kBinShift = 21;     // 11-bit key bins for the bound
 constexpr int kBins = 1 << (32 - kBinShift);
-constexpr int kFirstFiniteBin = 8;  // bins below hold -inf and NaN images only
-static_assert(kCap <= kThreads, "one listed candidate per thread");
+constexpr int kFirstFiniteBin = 4;  // bins below hold -inf and NaN images only
+static_assert(kCap <= kThreads, "one kept element per thread in the draw");
+static_assert(kMaxTiles % kThreads == 0, "tiles split evenly over threads");
+static_assert(kCands % kThreads == 0 && kCands * 8 <= kBins * 4, "candidate masses fit hist");
+static_assert(kBins % (4 * kThreads) == 0 && 4 * (kBins / kThreads) <= 64, "bound scan layout");
 
 struct RowInfo {
   float m;        // row max M
@@ -138,18 +144,293 @@ __device__ __forceinline__ void for_each_element(const void* row, int64_t V, boo
   for (int64_t v = done + t; v < V; v += kThreads) f(load_one<DT>(row, v), v);
 }
 
+// LDS of filter_rows_kernel.  hist is the bound histogram, then (as uint64) the
+// candidate masses of a walk, or the digit counts and masses of the radix select.
+struct RowsLds {
+  uint32_t hist[kBins];
+  uint32_t part[kThreads];
+  uint32_t ckey[kCands];
+  int32_t cidx[kCands];
+  float m, z;
+  int bin, count, rcount, ng, nk;
+  uint32_t above, rkey, tk, prefix, above_c;
+  uint64_t zk, above_m;
+};
+
+// Inclusive suffix sum over the 64 lanes of a wave (lane l: sum of lanes l..63).
+__device__ __forceinline__ uint32_t wave_suffix_u32(uint32_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_down(v, d);
+    if (lane + d < 64) v += o;
+  }
+  return v;
+}
+
+// Bin (11-bit key prefix) holding the k-th largest of the 2048 values lm (8 per
+// thread); -1 if k > 2048.  L.above receives the number of values in higher bins.
+// Every thread of the workgroup calls it.
+__device__ int kth_bin(RowsLds& L, const float (&lm)[8], int k) {
+  constexpr int PER = kBins / kThreads;  // bins summed per thread
+  const int t = threadIdx.x;
+  u32x4* h4 = reinterpret_cast<u32x4*>(L.hist);
+#pragma unroll
+  for (int i = 0; i < PER / 4; ++i) h4[t * (PER / 4) + i] = u32x4{0u, 0u, 0u, 0u};
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) atomicAdd(&L.hist[okey(lm[i]) >> kBinShift], 1u);
+  __syncthreads();
+  {
+    uint32_t ps = 0;
+#pragma unroll
+    for (int i = 0; i < PER / 4; ++i) {
+      const u32x4 v = h4[t * (PER / 4) + i];
+      ps += (v[0] + v[1]) + (v[2] + v[3]);
+    }
+    L.part[t] = ps;
+  }
+  __syncthreads();
+  if (t < 64) {
+    // lane l: the bins of threads 4l .. 4l+3, i.e. [4 PER l, 4 PER (l+1))
+    const uint32_t q = L.part[4 * t] + L.part[4 * t + 1] + L.part[4 * t + 2] + L.part[4 * t + 3];
+    const uint32_t s = wave_suffix_u32(q);
+    const uint64_t mask = __builtin_amdgcn_ballot_w64(k <= 2048 && s >= (uint32_t)k);
+    const int ls = mask ? 63 - __builtin_clzll(mask) : -1;  // uniform
+    if (ls < 0) {
+      if (t == 0) L.bin = -1;
+    } else {
+      // the chunk of lane ls (4 PER <= 64 bins), one bin per lane, suffix sums again
+      constexpr int CH = 4 * PER;
+      const uint32_t above_chunk = __shfl(s - q, ls);
+      const uint32_t hv = t < CH ? L.hist[CH * ls + t] : 0u;
+      const uint32_t sb = wave_suffix_u32(hv) + above_chunk;
+      const uint64_t m2 = __builtin_amdgcn_ballot_w64(t < CH && sb >= (uint32_t)k);
+      const int lb = 63 - __builtin_clzll(m2);  // non-empty: the chunk holds the k-th
+      if (t == lb) {
+        L.bin = CH * ls + lb;
+        L.above = sb - hv;
+      }
+    }
+  }
+  __syncthreads();
+  return L.bin;
+}
+
+// Key of the k-th largest of the 2048 values lm (k <= 2048), exact when at most
+// kThreads of them share its 12-bit bin (else the bin's lower edge, a smaller bound);
+// 0 when that value is -inf or k > 2048.  Uses hist and part.  Every thread calls it.
+__device__ uint32_t kth_key(RowsLds& L, const float (&lm)[8], int k) {
+  const int t = threadIdx.x;
+  const int bin = kth_bin(L, lm, k);
+  if (bin < kFirstFiniteBin) return 0u;
+  if (t == 0) {
+    L.rcount = 0;
+    L.rkey = 0u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t key = okey(lm[i]);
+    if ((int)(key >> kBinShift) == bin) {
+      const int slot = atomicAdd(&L.rcount, 1);
+      if (slot < kThreads) L.part[slot] = key;
+    }
+  }
+  __syncthreads();
+  const int n = L.rcount;
+  uint32_t result = (uint32_t)bin << kBinShift;
+  if (n <= kThreads) {
+    // the largest key of the bin with at least k values at or above it
+    if (t < n) {
+      const uint32_t key = L.part[t];
+      uint32_t cnt = L.above;
+      for (int q = 0; q < n; ++q) cnt += L.part[q] >= key ? 1u : 0u;
+      if (cnt >= (uint32_t)k) atomicMax(&L.rkey, key);
+    }
+    __syncthreads();
+    result = L.rkey;
+  }
+  __syncthreads();
+  return result;
+}
+
+// The 8 elements of a complete group of a row with 16-byte aligned groups.
+template <int DT>
+__device__ __forceinline__ void load8(const void* row, int64_t g, float (&x)[8]) {
+  if constexpr (DT == BSX_DTYPE_FP32) {
+    const f32x4 a = static_cast<const f32x4*>(row)[2 * g];
+    const f32x4 b = static_cast<const f32x4*>(row)[2 * g + 1];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      x[q] = a[q];
+      x[4 + q] = b[q];
+    }
+  } else {
+    const u32x4 w = static_cast<const u32x4*>(row)[g];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      x[2 * q] = lo_f32<DT>(w[q]);
+      x[2 * q + 1] = hi_f32<DT>(w[q]);
+    }
+  }
+}
+
+__device__ __forceinline__ void push_candidate(RowsLds& L, float x, int64_t v) {
+  const int slot = atomicAdd(&L.count, 1);
+  if (slot < kCands) {
+    L.ckey[slot] = okey(x);
+    L.cidx[slot] = (int32_t)v;
+  }
+}
+
+// Lists the row's elements >= a bound lf during the statistics pass.  In whole round
+// r = c0/8 each thread only sets bits 8r + i of a 128-bit register mask for its groups
+// t + 256*(c0 + i) whose maximum reaches the bound (at most 16 whole rounds); such
+// groups are rare, and their elements are read again after the pass (anything heavier
+// inside the pass's loop costs the loop occupancy).  Groups of the partial rounds list
+// their elements directly.
+constexpr int kMaxHitRounds = 16;
+
+template <int DT>
+struct Collector {
+  RowsLds* L;
+  float lf;
+  bool on;  // same value in every thread
+  int k;
+  uint64_t hits[2];
+  __device__ bool wants_first() const { return on; }
+  // The bound from the maxima of the first round's groups t + 256 i, i < 8: they are
+  // disjoint, so the k-th largest of the 2048 has at least k elements of the row at or
+  // above it, and so has t*.
+  __device__ void first(const float (&gm)[8]) {
+    const uint32_t kb = kth_key(*L, gm, k);
+    if (kb == 0u) on = false;
+    else lf = key_value(kb);
+  }
+  __device__ void round(int64_t c0, const float (&gm)[8]) {
+    if (!on) return;
+    uint64_t h = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h |= (gm[i] >= lf ? 1ull : 0ull) << i;
+    const int r = (int)(c0 / 8);
+    if (r < 8) hits[0] |= h << (8 * r);
+    else hits[1] |= h << (8 * (r - 8));
+  }
+  __device__ void group(int64_t g, const float* x, int n, float gm) {
+    if (!on || !(gm >= lf)) return;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < n && x[e] >= lf) push_candidate(*L, x[e], g * kGroup + e);
+  }
+};
+
+// Threshold from a complete list of the candidates [0, n) (every element of the row
+// at or above the smallest listed key is listed): each candidate gets the count and
+// mass of the listed keys at or above its own; t* is the largest key that reaches the
+// target.  Writes the kept indices (at most kCap, else the row gets no list).
+// Returns false (in every thread) when no listed key reaches the target.
+__device__ bool walk(RowsLds& L, int n, float c, float neg, bool use_k, bool use_p, int top_k,
+                     uint64_t target, int32_t* list_out) {
+  typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+  const int t = threadIdx.x;
+  uint64_t* cm = reinterpret_cast<uint64_t*>(L.hist);
+  constexpr int PER = kCands / kThreads;
+  const int n8 = (n + 7) & ~7;  // padded with key 0 (below every element's key), mass 0
+  if (t == 0) {
+    L.tk = 0u;
+    L.nk = 0;
+  }
+  for (int s = t; s < n8; s += kThreads) {
+    if (s < n) {
+      cm[s] = fx40(canon::weight(key_value(L.ckey[s]), c, neg));
+    } else {
+      cm[s] = 0ull;
+      L.ckey[s] = 0u;
+    }
+  }
+  __syncthreads();
+  if (!use_k) {
+    // top-p alone: t* is listed only if the listed mass reaches the target
+    uint64_t mine = 0ull;
+    for (int s = t; s < n; s += kThreads) mine += cm[s];
+    if (t == 0) L.zk = 0ull;
+    __syncthreads();
+    if (mine != 0ull) atomicAdd(reinterpret_cast<unsigned long long*>(&L.zk), (unsigned long long)mine);
+    __syncthreads();
+    const bool enough = L.zk >= target;
+    __syncthreads();
+    if (!enough) return false;
+  }
+  uint32_t key[PER];
+  uint32_t cnt[PER];
+  uint64_t mass[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int s = t + kThreads * j;
+    key[j] = s < n ? L.ckey[s] : 0xffffffffu;
+    cnt[j] = 0u;
+    mass[j] = 0ull;
+  }
+  if (n <= kThreads) {
+    // one candidate per thread; every listed key against it, 8 at a time from 16-byte
+    // reads; threads (and waves) without a candidate skip the loop
+    if (t < n) {
+      const u32x4* k4 = reinterpret_cast<const u32x4*>(L.ckey);
+      const u64x2* m2 = reinterpret_cast<const u64x2*>(cm);
+      for (int q = 0; q < n8; q += 8) {
+        const u32x4 ka = k4[q / 4], kb = k4[q / 4 + 1];
+        const u64x2 m01 = m2[q / 2], m23 = m2[q / 2 + 1], m45 = m2[q / 2 + 2], m67 = m2[q / 2 + 3];
+        const uint32_t kk[8] = {ka[0], ka[1], ka[2], ka[3], kb[0], kb[1], kb[2], kb[3]};
+        const uint64_t mm[8] = {m01[0], m01[1], m23[0], m23[1], m45[0], m45[1], m67[0], m67[1]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const bool ge = kk[e] >= key[0];
+          cnt[0] += ge ? 1u : 0u;
+          mass[0] += ge ? mm[e] : 0ull;
+        }
+      }
+    }
+  } else {
+    for (int q = 0; q < n; ++q) {
+      const uint32_t kq = L.ckey[q];
+      const uint64_t mq = cm[q];
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (kq >= key[j]) {
+          ++cnt[j];
+          mass[j] += mq;
+        }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (t + kThreads * j < n && reached(use_k, use_p, cnt[j], mass[j], top_k, target))
+      atomicMax(&L.tk, key[j]);
+  __syncthreads();
+  const uint32_t tk = L.tk;
+  // a finite element's key is never 0
+  if (tk == 0u) return false;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int s = t + kThreads * j;
+    if (s < n) {
+      if (key[j] == tk) L.zk = mass[j];  // equal keys hold equal masses
+      if (key[j] >= tk) {
+        const int slot = atomicAdd(&L.nk, 1);
+        if (slot < kCap) list_out[slot] = L.cidx[s];
+      }
+    }
+  }
+  __syncthreads();
+  if (t == 0 && L.nk > kCap) L.nk = -1;
+  __syncthreads();
+  return true;
+}
+
 template <int DT>
 __global__ void __launch_bounds__(kThreads) filter_rows_kernel(RowsArgs a) {
-  __shared__ __align__(16) uint32_t hist[kBins];  // bound histogram; reused by the radix select
-  __shared__ uint32_t part[kThreads];
-  __shared__ uint32_t ckey[kCap];
-  __shared__ int32_t cidx[kCap];
-  __shared__ uint64_t cmass[kCap];
-  __shared__ float s_m, s_z;
-  __shared__ int s_bin, s_count, s_nk;
-  __shared__ uint32_t s_t;
-  __shared__ uint64_t s_zk;
-
+  __shared__ __align__(16) RowsLds L;
   const int t = threadIdx.x;
   const int64_t r = blockIdx.x;
   const int64_t V = a.V;
@@ -160,144 +441,141 @@ __global__ void __launch_bounds__(kThreads) filter_rows_kernel(RowsArgs a) {
   const float c = a.c;
   const bool use_k = a.top_k > 0 && (int64_t)a.top_k < V;
   const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
+  const int k_eff = use_k ? a.top_k : kTopPProbe;
+  int32_t* list_out = a.lists + r * kCap;
 
-  // 1. canonical statistics and lane maxima
+  // 1. canonical statistics, listing candidates on the way when every thread has a
+  //    whole first round
+  if (t == 0) L.count = 0;
+  // Candidates are listed during the pass when every thread has a whole first round
+  // (the bound comes from it) and the hit masks cover the whole rounds.
+  const int64_t G_whole = V / kGroup;
+  Collector<DT> col{&L, INFINITY,
+                    vec && k_eff <= 2048 && ceil_div(G_whole, (int64_t)kThreads * 8) <= kMaxHitRounds,
+                    k_eff, {0ull, 0ull}};
   float lm[8];
-  acc::row_stats<DT, true>(row, V, vec, c, &s_m, &s_z, lm);
-  const float M = s_m, Z = s_z;
+  acc::row_stats<DT, true, Collector<DT>>(row, V, vec, c, &L.m, &L.z, lm, &col);
+  const float M = L.m, Z = L.z;
   const float neg = -(M * c);
   const uint64_t target = use_p ? (uint64_t)ceilf((a.top_p * Z) * 0x1p40f) : 0ull;
-
-  // 2. bound: the lower edge of the bin of the k_eff-th largest lane maximum
-  const int k_eff = use_k ? a.top_k : kTopPProbe;
-  for (int i = t; i < kBins; i += kThreads) hist[i] = 0u;
-  if (t == 0) {
-    s_count = 0;
-    s_nk = 0;
-    s_t = 0u;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 8; ++i) atomicAdd(&hist[okey(lm[i]) >> kBinShift], 1u);
-  __syncthreads();
-  {
-    uint32_t ps = 0;
-    for (int i = 0; i < kBins / kThreads; ++i) ps += hist[t * (kBins / kThreads) + i];
-    part[t] = ps;
-  }
-  __syncthreads();
-  if (t < 64) {
-    // lane l: bins [64 l, 64 l + 64); inclusive suffix sums over lanes
-    const uint32_t q = part[4 * t] + part[4 * t + 1] + part[4 * t + 2] + part[4 * t + 3];
-    uint32_t s = q;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t o = __shfl_down(s, d);
-      if (t + d < 64) s += o;
-    }
-    const uint64_t mask = __builtin_amdgcn_ballot_w64(k_eff <= 2048 && s >= (uint32_t)k_eff);
-    const int ls = mask ? 63 - __builtin_clzll(mask) : -1;
-    if (ls < 0) {
-      if (t == 0) s_bin = -1;
-    } else if (t == ls) {
-      uint32_t cum = s - q;
-      int bin = 64 * t;
-      for (int i = 64 * t + 63; i >= 64 * t; --i) {
-        cum += hist[i];
-        if (cum >= (uint32_t)k_eff) {
-          bin = i;
-          break;
-        }
-      }
-      s_bin = bin;
-    }
-  }
-  __syncthreads();
-  const bool all = s_bin < kFirstFiniteBin;
-  const float lf = all ? -INFINITY : key_value((uint32_t)s_bin << kBinShift);
-
-  // 3./4. list the elements >= L and walk them
-  bool listed = false;
-  if (!all || V <= kCap) {
-    for_each_element<DT>(row, V, vec, [&](float x, int64_t v) {
-      if (x >= lf) {
-        const int slot = atomicAdd(&s_count, 1);
-        if (slot < kCap) {
-          ckey[slot] = okey(x);
-          cidx[slot] = (int32_t)v;
-        }
-      }
-    });
+  if (col.on) {
+    // the noted groups of the whole rounds: their indices listed in LDS, then one
+    // group per thread read again (a single round trip for the usual few hundred)
+    if (t == 0) L.ng = 0;
     __syncthreads();
-    const int n = s_count;
-    if (n <= kCap) {
-      uint32_t key = 0u;
-      uint64_t mass = 0ull;
-      if (t < n) {
-        key = ckey[t];
-        cmass[t] = fx40(canon::weight(key_value(key), c, neg));
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      uint64_t h = col.hits[w];
+#pragma unroll 1
+      while (h != 0ull) {
+        const int bit = __builtin_ctzll(h);
+        h &= h - 1ull;
+        const int slot = atomicAdd(&L.ng, 1);
+        // bit 8r + i: group t + 256(8r + i)
+        if (slot < kBins) L.hist[slot] = (uint32_t)(t + 256 * (64 * w + bit));
       }
+    }
+    __syncthreads();
+    const int ng = min(L.ng, kBins);
+    for (int q = t; q < ng; q += kThreads) {
+      const int64_t g = L.hist[q];
+      float x[8];
+      load8<DT>(row, g, x);
+      uint32_t hb = 0u;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hb |= (x[e] >= col.lf ? 1u : 0u) << e;
+#pragma unroll 1
+      while (hb != 0u) {
+        const int e = __builtin_ctz(hb);
+        hb &= hb - 1u;
+        // the element again from cache: indexing x by a run-time e would put x in
+        // scratch memory
+        push_candidate(L, load_one<DT>(row, g * kGroup + e), g * kGroup + e);
+      }
+    }
+    __syncthreads();
+    if (L.ng > kBins && t == 0) L.count = kCands + 1;  // could not list them all
+    __syncthreads();
+  }
+
+  if (col.on && use_k && L.count > kThreads && L.count <= kCands) {
+    // With top-k on, t* is also at or above the k-th largest of the final lane maxima
+    // (each lane's maximum is at least that of its first group, so this bound is at or
+    // above the first one and the list stays complete above it): keep only those.
+    const uint32_t kb = kth_key(L, lm, k_eff);
+    const int n = L.count;
+    uint32_t ck[kCands / kThreads];
+    int32_t ci[kCands / kThreads];
+#pragma unroll
+    for (int j = 0; j < kCands / kThreads; ++j) {
+      const int s = t + kThreads * j;
+      ck[j] = s < n ? L.ckey[s] : 0u;
+      ci[j] = s < n ? L.cidx[s] : 0;
+    }
+    __syncthreads();
+    if (t == 0) L.count = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kCands / kThreads; ++j)
+      if (t + kThreads * j < n && ck[j] >= kb) {
+        const int slot = atomicAdd(&L.count, 1);
+        L.ckey[slot] = ck[j];
+        L.cidx[slot] = ci[j];
+      }
+    __syncthreads();
+  }
+
+  bool listed = false;
+  const bool early = col.on && L.count <= kCands;
+  if (early) listed = walk(L, L.count, c, neg, use_k, use_p, a.top_k, target, list_out);
+
+  // 2. otherwise the bound of all lane maxima, and a second read of the row
+  if (!listed && !early) {
+    const uint32_t kb = kth_key(L, lm, k_eff);
+    const bool all = kb == 0u;
+    if (!all || V <= kCands) {
+      const float lf = all ? -INFINITY : key_value(kb);
+      for_each_element<DT>(row, V, vec, [&](float x, int64_t v) {
+        if (x >= lf) push_candidate(L, x, v);
+      });
       __syncthreads();
-      if (t < n) {
-        uint32_t cnt = 0u;
-        for (int q = 0; q < n; ++q) {
-          if (ckey[q] >= key) {
-            ++cnt;
-            mass += cmass[q];
-          }
-        }
-        if (reached(use_k, use_p, cnt, mass, a.top_k, target)) atomicMax(&s_t, key);
-      }
-      __syncthreads();
-      const uint32_t tk = s_t;
-      // a finite element's key is never 0: 0 means no listed key reached the target
-      // (top-p alone with the nucleus below the bound)
-      if (tk != 0u) {
-        if (t < n && key == tk) s_zk = mass;  // equal keys hold equal masses
-        if (t < n && key >= tk) {
-          const int slot = atomicAdd(&s_nk, 1);
-          a.lists[r * kCap + slot] = cidx[t];
-        }
-        __syncthreads();
-        listed = true;
-      }
+      const int n = L.count;
+      if (n <= kCands) listed = walk(L, n, c, neg, use_k, use_p, a.top_k, target, list_out);
     }
   }
 
-  // 5. exact radix select
+  // 3. exact radix select
   if (!listed) {
-    uint32_t* hc = hist;                                  // [256]
-    uint64_t* hm = reinterpret_cast<uint64_t*>(hist + 256);  // [256]
-    __shared__ uint32_t s_prefix, s_above_c;
-    __shared__ uint64_t s_above_m;
+    uint32_t* hc = L.hist;                                     // [256]
+    uint64_t* hm = reinterpret_cast<uint64_t*>(L.hist + 256);  // [256]
     constexpr int NP = radix_passes<DT>();
     if (t == 0) {
-      s_prefix = 0u;
-      s_above_c = 0u;
-      s_above_m = 0ull;
+      L.prefix = 0u;
+      L.above_c = 0u;
+      L.above_m = 0ull;
     }
     for (int pass = 0; pass < NP; ++pass) {
       const int shift = 24 - 8 * pass;
       hc[t] = 0u;
       hm[t] = 0ull;
       __syncthreads();
-      const uint32_t prefix = s_prefix;
+      const uint32_t prefix = L.prefix;
       for_each_element<DT>(row, V, vec, [&](float x, int64_t) {
         const uint32_t key = okey(x);
         if (pass == 0 || (key >> (shift + 8)) == prefix) {
           const uint32_t d = (key >> shift) & 255u;
           atomicAdd(&hc[d], 1u);
           const uint64_t m = fx40(canon::weight(x, c, neg));
-          if (m != 0ull) atomicAdd(reinterpret_cast<unsigned long long*>(&hm[d]),
-                                   (unsigned long long)m);
+          if (m != 0ull)
+            atomicAdd(reinterpret_cast<unsigned long long*>(&hm[d]), (unsigned long long)m);
         }
       });
       __syncthreads();
       if (t == 0) {
-        uint32_t cum_c = s_above_c;
-        uint64_t cum_m = s_above_m;
+        uint32_t cum_c = L.above_c;
+        uint64_t cum_m = L.above_m;
         int chosen = -1;
-        uint32_t ch_prev_c = 0u, ch_c = 0u;
+        uint32_t ch_prev_c = 0u;
         uint64_t ch_prev_m = 0ull, ch_m = 0ull;
         for (int d = 255; d >= 0; --d) {
           if (hc[d] == 0u) continue;
@@ -308,25 +586,23 @@ __global__ void __launch_bounds__(kThreads) filter_rows_kernel(RowsArgs a) {
           chosen = d;  // the lowest non-empty digit so far
           ch_prev_c = pc;
           ch_prev_m = pm;
-          ch_c = cum_c;
           ch_m = cum_m;
           if (reached(use_k, use_p, cum_c, cum_m, a.top_k, target)) break;
         }
-        s_prefix = (pass == 0 ? 0u : (prefix << 8)) | (uint32_t)chosen;
-        s_above_c = ch_prev_c;
-        s_above_m = ch_prev_m;
-        s_zk = ch_m;
-        (void)ch_c;
+        L.prefix = (pass == 0 ? 0u : (prefix << 8)) | (uint32_t)chosen;
+        L.above_c = ch_prev_c;
+        L.above_m = ch_prev_m;
+        L.zk = ch_m;
       }
       __syncthreads();
     }
     if (t == 0) {
       constexpr int low_bits = 32 - 8 * NP;
-      uint32_t tk = low_bits == 0 ? s_prefix : (s_prefix << low_bits);
+      uint32_t tk = low_bits == 0 ? L.prefix : (L.prefix << low_bits);
       // the bits below the varying ones are 0 for positive values, 1 for negative
       if (low_bits > 0 && !(tk & 0x80000000u)) tk |= (1u << low_bits) - 1u;
-      s_t = tk;
-      s_nk = -1;
+      L.tk = tk;
+      L.nk = -1;
     }
     __syncthreads();
   }
@@ -334,9 +610,9 @@ __global__ void __launch_bounds__(kThreads) filter_rows_kernel(RowsArgs a) {
   if (t == 0) {
     RowInfo ri;
     ri.m = M;
-    ri.inv_k = 1.0f / (canon::u64_to_f32(s_zk) * 0x1p-40f);
-    ri.t_key = s_t;
-    ri.n_list = s_nk;
+    ri.inv_k = 1.0f / (canon::u64_to_f32(L.zk) * 0x1p-40f);
+    ri.t_key = L.tk;
+    ri.n_list = L.nk;
     a.info[r] = ri;
   }
 }
@@ -368,6 +644,13 @@ struct Filtered {
     const float x = load_one<DT>(row, v);
     return okey(x) >= tk ? canon::weight(x, c, nmc) * inv : 0.0f;
   }
+  // p of the 8 elements [v0, v0 + 8) of a 16-byte aligned row (v0 a multiple of 8)
+  __device__ __forceinline__ void p8(int64_t v0, float (&out)[8]) const {
+    float x[8];
+    load8<DT>(row, v0 / kGroup, x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = okey(x[e]) >= tk ? canon::weight(x[e], c, nmc) * inv : 0.0f;
+  }
 };
 
 template <int DT>
@@ -382,6 +665,30 @@ __device__ __forceinline__ Filtered<DT> filtered_row(const void* base, int64_t r
   return f;
 }
 
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m);
+  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += shfl_xor_u64(v, m);
+  return v;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ uint64_t wave_prefix_u64(uint64_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t lo = __shfl_up((uint32_t)v, d);
+    const uint32_t hi = __shfl_up((uint32_t)(v >> 32), d);
+    if (lane >= d) v += ((uint64_t)hi << 32) | lo;
+  }
+  return v;
+}
+
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* s_acc) {
   if (threadIdx.x == 0) *s_acc = 0ull;
   __syncthreads();
@@ -394,11 +701,12 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* s_acc) {
 
 template <int DT>
 __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
-  __shared__ int s_j, s_n, s_tok, s_last;
+  __shared__ int s_j, s_n, s_tok, s_last, s_tile, s_last_tile;
   __shared__ int32_t lv[kCap];
   __shared__ uint64_t lr[kCap];
-  __shared__ uint64_t s_acc;
+  __shared__ uint64_t s_acc, s_tbase;
   __shared__ uint64_t excl[kThreads];
+  __shared__ uint64_t tsum[kMaxTiles];
   const int b = blockIdx.x;
   const int t = threadIdx.x;
   const int k = a.k;
@@ -433,6 +741,7 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
       s_n = cnt;
       s_tok = INT_MAX;
       s_last = -1;
+      s_last_tile = 0;
     }
   }
   __syncthreads();
@@ -448,6 +757,30 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
     if (!with_q) return fx40(p);
     const float q = a.d_logits ? Q.p(v) : (v == xj ? 1.0f : 0.0f);
     return fx40(fmaxf(p - q, 0.0f));
+  };
+  // r_at of the 8 elements [v0, v0 + 8) (v0 a multiple of 8): one 16-byte load per row
+  // when the rows allow it
+  const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
+  const bool vec8 = (V * (int64_t)esz) % 16 == 0 && ((uintptr_t)P.row) % 16 == 0 &&
+                    (!(has_q && a.d_logits) || ((uintptr_t)Q.row) % 16 == 0);
+  auto r8 = [&](int64_t v0, bool with_q, uint64_t (&r)[8]) {
+    if (vec8 && v0 + 8 <= V) {
+      float p[8], q[8];
+      P.p8(v0, p);
+      if (with_q && a.d_logits) Q.p8(v0, q);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (!with_q) {
+          r[e] = fx40(p[e]);
+        } else {
+          const float qe = a.d_logits ? q[e] : (v0 + e == xj ? 1.0f : 0.0f);
+          r[e] = fx40(fmaxf(p[e] - qe, 0.0f));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = v0 + e < V ? r_at(v0 + e, with_q) : 0ull;
+    }
   };
   const float u = a.uniforms[trow0 + k];
   int tok = -1;
@@ -479,26 +812,48 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
       tok = s_tok != INT_MAX ? s_tok : s_last;
     }
   } else {
-    // no list: the whole row, thread t owning the contiguous chunk [lo, hi)
-    const int64_t chunk = ceil_div(V, (int64_t)kThreads);
-    const int64_t lo = min((int64_t)t * chunk, V);
-    const int64_t hi = min(lo + chunk, V);
+    // No list: the whole row, in tiles of 64 lanes x E consecutive elements (one wave
+    // per tile, at most kMaxTiles tiles): tile sums, their prefix, then the lane and
+    // the element inside the tile that holds the draw point.
+    const int E = kGroup * (int)ceil_div(V, (int64_t)kMaxTiles * 64 * kGroup);
+    const int64_t tile = 64LL * E;
+    const int ntiles = (int)ceil_div(V, tile);
+    const int wave = t >> 6, lane = t & 63;
+    auto lane_sum = [&](int T, bool with_q) -> uint64_t {
+      const int64_t v0 = T * tile + (int64_t)lane * E;
+      uint64_t s = 0ull;
+      for (int e0 = 0; e0 < E && v0 + e0 < V; e0 += 8) {
+        uint64_t r[8];
+        r8(v0 + e0, with_q, r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += r[e];
+      }
+      return s;
+    };
     uint64_t total = 0ull;
     bool with_q = has_q;
-    uint64_t sum = 0ull;
     for (int pass = 0; pass < 2; ++pass) {
       with_q = has_q && pass == 0;
       if (pass == 1 && !has_q) break;
-      sum = 0ull;
-      for (int64_t v = lo; v < hi; ++v) sum += r_at(v, with_q);
-      excl[t] = sum;
+      for (int T = wave; T < ntiles; T += kThreads / 64) {
+        const uint64_t s = wave_sum_u64(lane_sum(T, with_q));
+        if (lane == 0) tsum[T] = s;
+      }
+      __syncthreads();
+      // thread t: tiles [8t, 8t + 8); exclusive prefix of those groups
+      uint64_t mine = 0ull;
+      for (int i = 0; i < kMaxTiles / kThreads; ++i) {
+        const int T = t * (kMaxTiles / kThreads) + i;
+        if (T < ntiles) mine += tsum[T];
+      }
+      excl[t] = mine;
       __syncthreads();
       if (t == 0) {
         uint64_t run = 0ull;
         for (int i = 0; i < kThreads; ++i) {
-          const uint64_t s = excl[i];
+          const uint64_t x = excl[i];
           excl[i] = run;
-          run += s;
+          run += x;
         }
         s_acc = run;
       }
@@ -509,28 +864,63 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
     }
     if (total != 0ull) {
       const uint64_t tp = canon::draw_point(u, total);
-      const uint64_t e0 = excl[t];
-      if (sum != 0ull) {
-        if (tp >= e0 && tp < e0 + sum) {
-          uint64_t cum = e0;
-          for (int64_t v = lo; v < hi; ++v) {
-            cum += r_at(v, with_q);
-            if (cum > tp) {
-              s_tok = (int)v;
-              break;
-            }
+      if (t == 0) s_tile = -1;
+      __syncthreads();
+      // the tile whose running sum first exceeds tp (else the last non-empty tile)
+      uint64_t base = excl[t];
+      for (int i = 0; i < kMaxTiles / kThreads; ++i) {
+        const int T = t * (kMaxTiles / kThreads) + i;
+        if (T >= ntiles) break;
+        const uint64_t x = tsum[T];
+        if (x != 0ull) {
+          if (tp >= base && tp < base + x) {
+            s_tile = T;
+            s_tbase = base;
           }
+          atomicMax(&s_last_tile, T);
         }
-        int64_t last = -1;
-        for (int64_t v = hi - 1; v >= lo; --v)
-          if (r_at(v, with_q) != 0ull) {
-            last = v;
-            break;
-          }
-        atomicMax(&s_last, (int)last);
+        base += x;
       }
       __syncthreads();
-      tok = s_tok != INT_MAX ? s_tok : s_last;
+      const bool found = s_tile >= 0;
+      const int T = found ? s_tile : s_last_tile;
+      if (wave == 0) {
+        const uint64_t ls = lane_sum(T, with_q);
+        const uint64_t incl = wave_prefix_u64(ls);
+        const uint64_t lexcl = incl - ls;
+        if (found) {
+          const uint64_t tt = tp - s_tbase;
+          if (ls != 0ull && tt >= lexcl && tt < incl) {
+            uint64_t cum = lexcl;
+            const int64_t v0 = T * tile + (int64_t)lane * E;
+            bool done = false;
+            for (int e0 = 0; e0 < E && v0 + e0 < V && !done; e0 += 8) {
+              uint64_t r[8];
+              r8(v0 + e0, with_q, r);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                cum += r[e];
+                if (!done && cum > tt) {
+                  s_tok = (int)(v0 + e0 + e);
+                  done = true;
+                }
+              }
+            }
+          }
+        } else {
+          const uint64_t nz = __builtin_amdgcn_ballot_w64(ls != 0ull);
+          if (nz != 0ull && lane == 63 - __builtin_clzll(nz)) {
+            const int64_t v0 = T * tile + (int64_t)lane * E;
+            for (int e = E - 1; e >= 0; --e)
+              if (v0 + e < V && r_at(v0 + e, with_q) != 0ull) {
+                s_tok = (int)(v0 + e);
+                break;
+              }
+          }
+        }
+      }
+      __syncthreads();
+      tok = s_tok != INT_MAX ? s_tok : -1;
     }
   }
   if (t == 0) {

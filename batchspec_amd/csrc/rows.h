@@ -2,6 +2,8 @@
 // sampling-filter kernels (the arithmetic is specified in canon.h).
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 #include "canon.h"
 
@@ -60,10 +62,18 @@ __device__ __forceinline__ float load_one(const void* row, int64_t v) {
 // thread t owns lanes 8t+i (its groups t + 256*c, lane i = c mod 8).
 // ----------------------------------------------------------------------------
 // With LANES, lane_max[i] receives the maximum of lane 8t+i (-inf for a lane without
-// groups).
-template <int DT, bool LANES = false>
+// groups).  A Hook observes the pass without changing the statistics:
+// hook->round(c0, gm) in each whole round (groups t + 256*(c0 + i), i < 8, gm[i]
+// their maxima), hook->group(g, x, n, gm) for each group of the remaining partial
+// rounds (x its n elements), and, when hook->wants_first() (same value in every
+// thread) and every thread has a whole first round, hook->first(gm) before that
+// round's hook->round (called by every thread; the first round runs outside the loop).
+struct NoRowHook {};
+
+template <int DT, bool LANES = false, typename Hook = NoRowHook>
 __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* out_m,
-                          float* out_z, float* lane_max = nullptr) {
+                          float* out_z, float* lane_max = nullptr, Hook* hook = nullptr) {
+  constexpr bool HOOKED = !std::is_same<Hook, NoRowHook>::value;
   __shared__ float wave_val[4];
   const int t = threadIdx.x;
   const int64_t G = ceil_div(V, kGroup);
@@ -80,7 +90,8 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
     // found with one ballot for the 8 lanes; then every weight, in the canonical order.
     const int64_t G_whole = V / kGroup;
     constexpr int VW = DT == BSX_DTYPE_FP32 ? 2 : 1;
-    for (; (int64_t)t + 256 * (c0 + 7) < G_whole; c0 += 8) {
+    auto whole_round = [&](int64_t c0, auto first_tag) {
+      constexpr bool FIRST = decltype(first_tag)::value;
       u32x4 w[8][VW];
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -112,6 +123,10 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
                                           __builtin_elementwise_maximum(x[i][6], x[i][7])));
         need |= gm[i] > st[i].m;
       }
+      if constexpr (HOOKED) {
+        if constexpr (FIRST) hook->first(gm);
+        hook->round(c0, gm);
+      }
       if (__builtin_amdgcn_ballot_w64(need) != 0) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -129,7 +144,16 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
         for (int e = 1; e < 8; ++e) gs = gs + canon::weight(x[i][e], c, neg_rho);
         st[i].s = st[i].s + gs;
       }
+    };
+    if constexpr (HOOKED) {
+      // The first round on its own when every thread has one and the hook wants it
+      // (hook->first(gm) is called by every thread, outside the loop).
+      if (255 + 256 * 7 < G_whole && hook->wants_first()) {
+        whole_round(0, std::true_type());
+        c0 = 8;
+      }
     }
+    for (; (int64_t)t + 256 * (c0 + 7) < G_whole; c0 += 8) whole_round(c0, std::false_type());
   }
   for (; (int64_t)t + 256 * c0 < G; c0 += 8) {
 #pragma unroll
@@ -147,6 +171,7 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
         } else {
           canon::lane_update(st[i], x, n, gm, c);
         }
+        if constexpr (HOOKED) hook->group(g, x, n, gm);
       }
     }
   }

@@ -368,6 +368,15 @@ def main() -> int:
         result["stochastic_accept"] = {"us": round(t_st, 2), "GB/s": round(sbytes / t_st / 1e3, 1),
                                        "frac": round(sbytes / t_st / 1e3 / HBM_PEAK_GBS, 4),
                                        "bytes": sbytes}
+        # the same acceptance with the reference's default filters (top_k=20, top_p=0.95)
+        # applied to both distributions
+        sf_us = time_events(lambda i: bsx.sampling.chain_speculative_sampling_from_logits(
+            s.draft_logits, s.draft_tokens, s.target_logits, 1.0, uniforms=s.uniforms,
+            top_k=20, top_p=0.95), max(5, args.steps // 3), 2)
+        t_sf = sum(sf_us) / len(sf_us)
+        result["stochastic_accept_top_k20_top_p095"] = {
+            "us": round(t_sf, 2), "GB/s": round(sbytes / t_sf / 1e3, 1),
+            "frac": round(sbytes / t_sf / 1e3 / HBM_PEAK_GBS, 4), "bytes": sbytes}
         del s
 
     if args.extra_configs:
