@@ -38,6 +38,7 @@ HIP_SOURCES = {
     "attn.hip": [],
     "append.hip": [],
     "collate.hip": [],
+    "masks.hip": [],
     "accept.hip": ["-ffp-contract=off"],
     "filter.hip": ["-ffp-contract=off"],
 }

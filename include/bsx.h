@@ -264,6 +264,20 @@ int bsx_softmax(const void* logits_d, int dtype, float temperature, int64_t rows
                 int64_t vocab, float* probs_d, void* ws_d, int64_t ws_bytes,
                 void* stream);
 
+/* Draft-tree masks on the device: replaces the MTP mask and position ids of
+ * MTPEngine._setup_common_attn_mask_and_position_ids (batchspec/backends/mtp_engine.py:
+ * 172-208) and the per-request ones/mask concatenation before plan() (:410-417), and
+ * the EAGLE tree masks, from parent arrays.
+ *   parents_d [B, parents_stride] int32 (parents_stride 0: one array [n] shared by
+ *   every request); parent[i] < i, -1 for a node hanging off the cached prefix (a
+ *   parent >= i or < -1 ends the chain there).  n <= 32.
+ *   Outputs: words_d [B*n] uint32, bit j = token j is the token or an ancestor (the
+ *   attention plan's tree_mask_words); positions_d [B*n] int64 (or NULL) =
+ *   cachelens_d[b] (0 if NULL) + depth. */
+int bsx_tree_masks(const int32_t* parents_d, int64_t parents_stride, int n,
+                   const int32_t* cachelens_d, int B, uint32_t* words_d,
+                   int64_t* positions_d, void* stream);
+
 /* Top-k / top-p renormalisation (batchspec/backends/utils/sampling.py:50-56: top-p on
  * the full softmax(logits/T), then top-k on the renormalised distribution; top-k is on
  * iff 0 < top_k < vocab, top-p iff 0 < top_p < 1) fused into the stochastic acceptance

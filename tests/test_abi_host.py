@@ -192,6 +192,18 @@ def test_tree_words_match_oracle_ancestor_mask():
         assert depth.max() <= 6
 
 
+@pytest.mark.parametrize("k", [1, 2, 3, 4])
+def test_mtp_parents_give_the_mtp_mask(k):
+    # the MTP layout read as a tree: its ancestor relation and depths are the closed form
+    # of mtp_engine.py:172-208 (pinned by the k = 2 known answer of mtp_engine.py:360-368)
+    par = masks.mtp_parents(k)
+    m, depth = OM.tree_ancestor_mask(par)
+    rm, rpos = OM.mtp_mask(k)
+    np.testing.assert_array_equal(m, rm)
+    np.testing.assert_array_equal(depth, rpos)
+    assert np.all(par < np.arange(par.size))
+
+
 def test_custom_mask_packing_of_mtp_verify_mask():
     k = 4
     cachelens = [7, 0, 30]
