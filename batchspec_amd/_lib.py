@@ -99,6 +99,8 @@ SIGNATURES = {
     "bsx_chain_speculative_sampling_logits": (c_int, [_P, _P, _P, c_int, c_float, _P, c_int, c_int,
                                                       c_int64, _P, _P, _P, _P, c_int64, _P]),
     "bsx_tree_masks": (c_int, [_P, c_int64, c_int, _P, c_int, _P, _P, _P]),
+    "bsx_page_table_update": (c_int, [_P, _P, _P, _P, c_int32, c_int, c_int, c_int, c_int, _P, _P,
+                                      _P, _P]),
     "bsx_filter_ws_bytes": (c_int64, [c_int64]),
     "bsx_chain_filtered_ws_bytes": (c_int64, [c_int, c_int, c_int64]),
     "bsx_chain_speculative_sampling_filtered": (c_int, [_P, _P, _P, c_int, c_float, c_int, c_float,

@@ -39,6 +39,7 @@ HIP_SOURCES = {
     "append.hip": [],
     "collate.hip": [],
     "masks.hip": [],
+    "page_table.hip": [],
     "accept.hip": ["-ffp-contract=off"],
     "filter.hip": ["-ffp-contract=off"],
 }

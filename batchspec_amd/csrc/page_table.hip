@@ -1,0 +1,148 @@
+// Sync-free page-table update (a "next" row of the path).
+//
+// Replaces PageTable.insert_kv / delete_kv (batchspec/backends/base/page_table.py:55-137)
+// with PageManager.allocate / free (batchspec/backends/utils/paging.py:155-277), which
+// read results back to the host several times per step (.item(), nonzero, data-dependent
+// tensor sizes).  The same state lives in fixed-size device buffers and one workgroup
+// updates it:
+//   per request r: total = (pages_r - 1) * page_size + last_r (+ dec or - del);
+//   insert: pages only grow (the tail pages of the new total are appended);
+//   delete: total clamped at 0, tail pages dropped;  pages >= 1 always;
+//   last_r = (total - 1) % page_size + 1 (0 for an empty request);
+//   cachelens_r = max(cachelens_r +/- d_r, 0);
+//   when no d_r > 0, nothing changes (the reference returns early);
+//   an insert that would give some request more than max_pages pages changes nothing
+//   and increments *errors (the reference raises before touching its state).
+// Page k of request r has id r * max_pages + k (the reference allocator's ids), so the
+// packed CSR (indptr = exclusive scan of page counts, indices) is rebuilt from the counts.
+#include "common.h"
+
+namespace bsx {
+namespace pt {
+
+constexpr int kThreads = 1024;
+
+struct Args {
+  int32_t* num_pages;
+  int32_t* last_len;
+  int32_t* cachelens;  // may be null
+  const int32_t* d;    // [B] or null (then d_scalar)
+  int32_t d_scalar;
+  int sign;            // +1 insert, -1 delete
+  int B, page_size, max_pages;
+  int32_t* indptr;     // [B + 1]
+  int32_t* indices;    // [B * max_pages]
+  int32_t* errors;     // may be null
+};
+
+__global__ void __launch_bounds__(kThreads) page_table_kernel(Args a) {
+  __shared__ int32_t s_scan[kThreads];
+  __shared__ int32_t s_base;
+  const int t = threadIdx.x;
+  const int ps = a.page_size;
+  auto delta = [&](int r) -> int32_t { return a.d ? a.d[r] : a.d_scalar; };
+
+  // anything to do? and would any request overflow?
+  int any_pos = 0, over = 0;
+  for (int r = t; r < a.B; r += kThreads) {
+    const int32_t d = delta(r);
+    any_pos |= d > 0;
+    if (a.sign > 0) {
+      const int64_t total = (int64_t)(a.num_pages[r] - 1) * ps + a.last_len[r] + d;
+      const int64_t full = total > 0 ? (total - 1) / ps : 0;
+      const int64_t pages = max((int64_t)a.num_pages[r], full + 1);
+      over |= pages > a.max_pages;
+    }
+  }
+  any_pos = __syncthreads_or(any_pos);
+  over = __syncthreads_or(over);
+  if (!any_pos) return;
+  if (over) {
+    if (t == 0 && a.errors) a.errors[0] += 1;
+    return;
+  }
+
+  // new counts and tails (each thread owns its requests)
+  for (int r = t; r < a.B; r += kThreads) {
+    const int32_t d = delta(r);
+    const int32_t old_pages = a.num_pages[r];
+    int64_t total = (int64_t)(old_pages - 1) * ps + a.last_len[r] + (int64_t)a.sign * d;
+    if (total < 0) total = 0;
+    const int64_t full = total > 0 ? (total - 1) / ps : 0;
+    const int32_t tail = total > 0 ? (int32_t)((total - 1) % ps + 1) : 0;
+    const int32_t pages = a.sign > 0 ? max(old_pages, (int32_t)(full + 1))
+                                     : min(old_pages, (int32_t)(full + 1));
+    a.num_pages[r] = pages;
+    a.last_len[r] = tail;
+    if (a.cachelens) {
+      const int64_t cl = (int64_t)a.cachelens[r] + (int64_t)a.sign * d;
+      a.cachelens[r] = cl > 0 ? (int32_t)cl : 0;
+    }
+  }
+  __syncthreads();
+
+  // indptr: exclusive scan of the page counts, kThreads requests at a time
+  if (t == 0) s_base = 0;
+  __syncthreads();
+  for (int r0 = 0; r0 < a.B; r0 += kThreads) {
+    const int r = r0 + t;
+    const int32_t v = r < a.B ? a.num_pages[r] : 0;
+    s_scan[t] = v;
+    __syncthreads();
+    for (int off = 1; off < kThreads; off <<= 1) {
+      const int32_t o = t >= off ? s_scan[t - off] : 0;
+      __syncthreads();
+      s_scan[t] += o;
+      __syncthreads();
+    }
+    const int32_t base = s_base;
+    if (r < a.B) a.indptr[r] = base + s_scan[t] - v;
+    __syncthreads();
+    if (t == kThreads - 1) s_base = base + s_scan[t];
+    __syncthreads();
+  }
+  if (t == 0) a.indptr[a.B] = s_base;
+  __syncthreads();
+
+  // indices: request by request, its pages spread over the workgroup
+  for (int r = 0; r < a.B; ++r) {
+    const int32_t beg = a.indptr[r];
+    const int32_t n = a.num_pages[r];
+    for (int k = t; k < n; k += kThreads) a.indices[beg + k] = r * a.max_pages + k;
+  }
+}
+
+}  // namespace pt
+}  // namespace bsx
+
+using namespace bsx;
+
+extern "C" int bsx_page_table_update(int32_t* num_pages_d, int32_t* last_len_d,
+                                     int32_t* cachelens_d, const int32_t* d_d,
+                                     int32_t d_scalar, int sign, int B, int page_size,
+                                     int max_pages, int32_t* indptr_d, int32_t* indices_d,
+                                     int32_t* errors_d, void* stream) {
+  BSX_REQUIRE(B >= 0, BSX_ERR_INVALID, "bad batch %d", B);
+  if (B == 0) return BSX_OK;
+  BSX_REQUIRE(sign == 1 || sign == -1, BSX_ERR_INVALID, "sign must be +1 (insert) or -1 (delete)");
+  BSX_REQUIRE(page_size > 0 && max_pages > 0, BSX_ERR_INVALID, "bad page_size or max_pages");
+  BSX_REQUIRE((int64_t)B * max_pages < (1LL << 31), BSX_ERR_UNSUPPORTED, "page table too large");
+  BSX_REQUIRE(num_pages_d && last_len_d && indptr_d && indices_d, BSX_ERR_INVALID,
+              "null pointer");
+  pt::Args a;
+  a.num_pages = num_pages_d;
+  a.last_len = last_len_d;
+  a.cachelens = cachelens_d;
+  a.d = d_d;
+  a.d_scalar = d_scalar;
+  a.sign = sign;
+  a.B = B;
+  a.page_size = page_size;
+  a.max_pages = max_pages;
+  a.indptr = indptr_d;
+  a.indices = indices_d;
+  a.errors = errors_d;
+  hipLaunchKernelGGL(pt::page_table_kernel, dim3(1), dim3(pt::kThreads), 0, as_stream(stream), a);
+  BSX_LAUNCH_CHECK();
+  return BSX_OK;
+}

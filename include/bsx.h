@@ -264,6 +264,21 @@ int bsx_softmax(const void* logits_d, int dtype, float temperature, int64_t rows
                 int64_t vocab, float* probs_d, void* ws_d, int64_t ws_bytes,
                 void* stream);
 
+/* Sync-free page-table update: PageTable.insert_kv (sign +1) / delete_kv (sign -1)
+ * (batchspec/backends/base/page_table.py:55-137) with PageManager.allocate / free
+ * (batchspec/backends/utils/paging.py:155-277), in one kernel on fixed-size buffers.
+ *   num_pages_d, last_len_d, cachelens_d (or NULL) [B] int32: updated in place;
+ *   d_d [B] int32 lengths, or NULL to use d_scalar for every request;
+ *   indptr_d [B+1], indices_d [B*max_pages]: the rebuilt CSR (page k of request r is
+ *   r*max_pages + k, the reference allocator's ids).
+ * No update happens when no length is positive (the reference returns early), or when
+ * an insert would exceed max_pages for some request: then *errors_d (if given) is
+ * incremented, where the reference raises RuntimeError. */
+int bsx_page_table_update(int32_t* num_pages_d, int32_t* last_len_d, int32_t* cachelens_d,
+                          const int32_t* d_d, int32_t d_scalar, int sign, int B,
+                          int page_size, int max_pages, int32_t* indptr_d,
+                          int32_t* indices_d, int32_t* errors_d, void* stream);
+
 /* Draft-tree masks on the device: replaces the MTP mask and position ids of
  * MTPEngine._setup_common_attn_mask_and_position_ids (batchspec/backends/mtp_engine.py:
  * 172-208) and the per-request ones/mask concatenation before plan() (:410-417), and
