@@ -37,6 +37,8 @@ struct Args {
 
 __global__ void __launch_bounds__(kThreads) page_table_kernel(Args a) {
   __shared__ int32_t s_scan[kThreads];
+  __shared__ int32_t s_pages[kThreads];
+  __shared__ int32_t s_wave[kThreads / 64];
   __shared__ int32_t s_base;
   const int t = threadIdx.x;
   const int ps = a.page_size;
@@ -81,35 +83,50 @@ __global__ void __launch_bounds__(kThreads) page_table_kernel(Args a) {
   }
   __syncthreads();
 
-  // indptr: exclusive scan of the page counts, kThreads requests at a time
+  // indptr (exclusive scan of the page counts) and indices, kThreads requests at a
+  // time; each chunk's counts and starts stay in LDS for the index writes
   if (t == 0) s_base = 0;
   __syncthreads();
   for (int r0 = 0; r0 < a.B; r0 += kThreads) {
     const int r = r0 + t;
     const int32_t v = r < a.B ? a.num_pages[r] : 0;
-    s_scan[t] = v;
-    __syncthreads();
-    for (int off = 1; off < kThreads; off <<= 1) {
-      const int32_t o = t >= off ? s_scan[t - off] : 0;
-      __syncthreads();
-      s_scan[t] += o;
-      __syncthreads();
+    s_pages[t] = v;
+    // inclusive scan: within each wave by shuffles, then over the wave totals
+    const int lane = t & 63, wave = t >> 6;
+    int32_t x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int32_t o = __shfl_up(x, d);
+      if (lane >= d) x += o;
     }
+    if (lane == 63) s_wave[wave] = x;
+    __syncthreads();
+    if (t < 64) {
+      int32_t w = t < kThreads / 64 ? s_wave[t] : 0;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int32_t o = __shfl_up(w, d);
+        if (t >= d) w += o;
+      }
+      if (t < kThreads / 64) s_wave[t] = w;  // inclusive over waves
+    }
+    __syncthreads();
+    s_scan[t] = x + (wave > 0 ? s_wave[wave - 1] : 0);
+    __syncthreads();
     const int32_t base = s_base;
     if (r < a.B) a.indptr[r] = base + s_scan[t] - v;
+    const int nr = min(kThreads, a.B - r0);
+    // the chunk's requests one after another, each request's pages over the workgroup
+    for (int q = 0; q < nr; ++q) {
+      const int32_t n = s_pages[q];
+      const int32_t beg = base + s_scan[q] - n;
+      for (int k = t; k < n; k += kThreads) a.indices[beg + k] = (r0 + q) * a.max_pages + k;
+    }
     __syncthreads();
     if (t == kThreads - 1) s_base = base + s_scan[t];
     __syncthreads();
   }
   if (t == 0) a.indptr[a.B] = s_base;
-  __syncthreads();
-
-  // indices: request by request, its pages spread over the workgroup
-  for (int r = 0; r < a.B; ++r) {
-    const int32_t beg = a.indptr[r];
-    const int32_t n = a.num_pages[r];
-    for (int k = t; k < n; k += kThreads) a.indices[beg + k] = r * a.max_pages + k;
-  }
 }
 
 }  // namespace pt

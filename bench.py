@@ -149,6 +149,45 @@ def extra_configs(dev, iters: int):
                                                           window_tokens=512),
                                           [view_bytes(b) for b in s3a], iters)
     del s3a
+
+    # Verify-step plumbing: the config-4 tree masks built on the device, and one step's
+    # page-table update (insert the 25 MTP tokens, delete the rejected ones) at the
+    # config-2 batch, against the host-synchronising torch mirror of the reference.
+    import time
+    from batchspec_amd.masks import tree_masks
+    from batchspec_amd.page_table import DevicePageTable, PageTable
+    from batchspec_amd.workloads import random_tree_parents
+    rng = np.random.default_rng(1004)
+    par = torch.from_numpy(np.stack([random_tree_parents(32, rng) for _ in range(32)])
+                           .astype(np.int32)).to(dev)
+    cl = torch.from_numpy(rng.integers(2048, 8192, 32).astype(np.int32)).to(dev)
+    us = time_events(lambda i: tree_masks(par, cl), iters, 3)
+    out["config4_tree_masks"] = {"us": round(sum(us) / len(us), 2), "requests": 32, "nodes": 32}
+    acc = torch.from_numpy(rng.integers(1, 6, 64).astype(np.int32)).to(dev)
+    rej = 25 - acc
+    dpt = DevicePageTable(16, 64, 600, dev)
+    dpt.insert_kv(torch.from_numpy(rng.integers(1024, 4096, 64).astype(np.int32)).to(dev))
+
+    def step_dev(i):
+        dpt.insert_kv(25)
+        dpt.delete_kv(rej)
+    us = time_events(step_dev, iters, 3)
+    dpt.check()
+    hpt = PageTable(16, 64, 600, dev)
+    hpt.clear_kv()
+    hpt.insert_kv(torch.from_numpy(rng.integers(1024, 4096, 64).astype(np.int32)).to(dev))
+    for _ in range(3):
+        hpt.insert_kv(25)
+        hpt.delete_kv(rej)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        hpt.insert_kv(25)
+        hpt.delete_kv(rej)
+    torch.cuda.synchronize()
+    host_us = (time.perf_counter() - t0) / iters * 1e6
+    out["page_table_step"] = {"device_us": round(sum(us) / len(us), 2),
+                              "torch_mirror_wall_us": round(host_us, 1), "requests": 64}
     return out
 
 
