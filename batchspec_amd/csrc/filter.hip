@@ -144,6 +144,30 @@ __device__ __forceinline__ void for_each_element(const void* row, int64_t V, boo
   for (int64_t v = done + t; v < V; v += kThreads) f(load_one<DT>(row, v), v);
 }
 
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m);
+  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += shfl_xor_u64(v, m);
+  return v;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ uint64_t wave_prefix_u64(uint64_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t lo = __shfl_up((uint32_t)v, d);
+    const uint32_t hi = __shfl_up((uint32_t)(v >> 32), d);
+    if (lane >= d) v += ((uint64_t)hi << 32) | lo;
+  }
+  return v;
+}
+
 // LDS of filter_rows_kernel.  hist is the bound histogram, then (as uint64) the
 // candidate masses of a walk, or the digit counts and masses of the radix select.
 struct RowsLds {
@@ -665,30 +689,6 @@ __device__ __forceinline__ Filtered<DT> filtered_row(const void* base, int64_t r
   return f;
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  const uint32_t lo = __shfl_xor((uint32_t)v, m);
-  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += shfl_xor_u64(v, m);
-  return v;
-}
-
-// Inclusive prefix sum over the 64 lanes of a wave.
-__device__ __forceinline__ uint64_t wave_prefix_u64(uint64_t v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t lo = __shfl_up((uint32_t)v, d);
-    const uint32_t hi = __shfl_up((uint32_t)(v >> 32), d);
-    if (lane >= d) v += ((uint64_t)hi << 32) | lo;
-  }
-  return v;
-}
-
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* s_acc) {
   if (threadIdx.x == 0) *s_acc = 0ull;
   __syncthreads();
@@ -835,9 +835,21 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
     for (int pass = 0; pass < 2; ++pass) {
       with_q = has_q && pass == 0;
       if (pass == 1 && !has_q) break;
-      for (int T = wave; T < ntiles; T += kThreads / 64) {
-        const uint64_t s = wave_sum_u64(lane_sum(T, with_q));
-        if (lane == 0) tsum[T] = s;
+      // U tiles per wave at a time: their loads go out together
+      constexpr int U = 8;
+      for (int T0 = wave; T0 < ntiles; T0 += (kThreads / 64) * U) {
+        uint64_t ls[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int T = T0 + (kThreads / 64) * u;
+          ls[u] = lane_sum(T < ntiles ? T : T0, with_q);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int T = T0 + (kThreads / 64) * u;
+          const uint64_t s = wave_sum_u64(ls[u]);
+          if (lane == 0 && T < ntiles) tsum[T] = s;
+        }
       }
       __syncthreads();
       // thread t: tiles [8t, 8t + 8); exclusive prefix of those groups
