@@ -951,12 +951,15 @@ __global__ void __launch_bounds__(256) merge_kernel(Params p) {
   constexpr int TPR = D / 8;  // threads per row (8 columns each)
   constexpr int RPB = 256 / TPR;
   constexpr int U = 8;        // parts loaded per round
-  const int b = ld_uniform(p.blob, p.off_merge_seqs + blockIdx.x);
+  // the request's merge record {first part, end of parts, first query token, query
+  // tokens}: one scalar load
+  typedef const u32x4 __attribute__((address_space(4)))* const_u4_ptr;
+  const u32x4 rec = ((const_u4_ptr)(p.blob + p.off_merge_seqs))[blockIdx.x];
   const int h = blockIdx.y;
-  const int pbeg = ld_uniform(p.blob, p.off_part_indptr + b);
-  const int pend = ld_uniform(p.blob, p.off_part_indptr + b + 1);
-  const int qo_start = ld_uniform(p.blob, p.off_seq + b * 4 + 0);
-  const int qo_len = ld_uniform(p.blob, p.off_seq + b * 4 + 1);
+  const int pbeg = (int)rec[0];
+  const int pend = (int)rec[1];
+  const int qo_start = (int)rec[2];
+  const int qo_len = (int)rec[3];
   const int g = p.group;
   const int row = blockIdx.z * RPB + threadIdx.x / TPR;
   if (row >= qo_len * g) return;

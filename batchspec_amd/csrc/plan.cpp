@@ -11,7 +11,8 @@
 //   seq[batch][4]      qo_start, qo_len, kv_len, page_start
 //   seg_indptr[ctas+1] segments of workgroup w are [seg_indptr[w], seg_indptr[w+1])
 //   segments[S][4]     request, first tile, end tile, partial slot (-1 = final)
-//   merge_seqs[M]      requests whose kv range spans several segments
+//   merge[M][4]        per request whose kv range spans several segments (16-byte
+//                      aligned): first partial slot, end slot, qo_start, qo_len
 //   part_indptr[b+1]   partial slots of request b are [part_indptr[b], part_indptr[b+1])
 #include <stdarg.h>
 #include <stdint.h>
@@ -99,9 +100,10 @@ static int waves_per_simd(int head_dim, int qrow_tile) {
 extern "C" int64_t bsx_attn_plan_ints_bound(int batch, int num_cus) {
   if (batch < 0 || num_cus < 1) return -1;
   const int64_t num_ctas = (int64_t)num_cus * 16;
-  // seq 4B + seg_indptr (W+1) + segments 4*(2W + 2B) + merge B + part_indptr (B+1)
-  return 4LL * batch + (num_ctas + 1) + 4LL * (2 * num_ctas + 2LL * batch) + batch + (batch + 1) +
-         16;
+  // seq 4B + seg_indptr (W+1) + segments 4*(2W + 2B) + merge records 4B (+3 to align)
+  // + part_indptr (B+1)
+  return 4LL * batch + (num_ctas + 1) + 4LL * (2 * num_ctas + 2LL * batch) + 4LL * batch + 3 +
+         (batch + 1) + 16;
 }
 
 extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
@@ -247,7 +249,7 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   int nseg = 0;
   for (const auto& v : per_cta) nseg += (int)v.size();
   const int64_t need =
-      4LL * batch + (W + 1) + 4LL * nseg + (int64_t)merge_seqs.size() + (batch + 1);
+      4LL * batch + (W + 1) + 4LL * nseg + 3 + 4LL * (int64_t)merge_seqs.size() + (batch + 1);
   PLAN_REQUIRE(need <= blob_capacity_ints, BSX_ERR_CAPACITY,
                "plan blob needs %lld int32 entries, capacity %lld", (long long)need,
                (long long)blob_capacity_ints);
@@ -256,8 +258,8 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   const int off_seq = 0;
   const int off_seg_indptr = off_seq + 4 * batch;
   const int off_segments = off_seg_indptr + W + 1;
-  const int off_merge = off_segments + 4 * nseg;
-  const int off_part = off_merge + (int)merge_seqs.size();
+  const int off_merge = (off_segments + 4 * nseg + 3) & ~3;  // 16-byte records
+  const int off_part = off_merge + 4 * (int)merge_seqs.size();
   for (int b = 0; b < batch; ++b) {
     blob[off_seq + 4 * b + 0] = qo_indptr_h[b];
     blob[off_seq + 4 * b + 1] = qo_len[b];
@@ -276,7 +278,14 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
     }
   }
   blob[off_seg_indptr + W] = si;
-  for (size_t i = 0; i < merge_seqs.size(); ++i) blob[off_merge + (int)i] = merge_seqs[i];
+  for (int i = off_segments + 4 * nseg; i < off_merge; ++i) blob[i] = 0;
+  for (size_t i = 0; i < merge_seqs.size(); ++i) {
+    const int b = merge_seqs[i];
+    blob[off_merge + 4 * (int)i + 0] = part_indptr[b];
+    blob[off_merge + 4 * (int)i + 1] = part_indptr[b + 1];
+    blob[off_merge + 4 * (int)i + 2] = qo_indptr_h[b];
+    blob[off_merge + 4 * (int)i + 3] = qo_len[b];
+  }
   for (int b = 0; b <= batch; ++b) blob[off_part + b] = part_indptr[b];
 
   memset(out, 0, sizeof(*out));

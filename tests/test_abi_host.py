@@ -82,9 +82,15 @@ def test_plan_covers_every_tile_once_and_balances(cus):
     assert cost.max() <= np.ceil(ideal) + 2 * SEG_COST + 1, (cost.max(), ideal)
     assert plan.num_ctas <= cus * 2
     assert plan.total_tiles == int(np.sum(kv_tiles))
-    merge = blob[plan.off_merge_seqs: plan.off_merge_seqs + plan.num_split_requests]
+    # merge records (16-byte aligned): first slot, end slot, qo_start, qo_len per split request
+    assert plan.off_merge_seqs % 4 == 0
+    merge = blob[plan.off_merge_seqs: plan.off_merge_seqs + 4 * plan.num_split_requests].reshape(-1, 4)
     split = [b for b in range(B) if np.sum(segs[:, 0] == b) > 1]
-    assert merge.tolist() == split
+    pip_ = blob[plan.off_part_indptr: plan.off_part_indptr + B + 1]
+    assert merge[:, 0].tolist() == [int(pip_[b]) for b in split]
+    assert merge[:, 1].tolist() == [int(pip_[b + 1]) for b in split]
+    assert merge[:, 2].tolist() == [int(qo[b]) for b in split]
+    assert merge[:, 3].tolist() == [int(qo[b + 1] - qo[b]) for b in split]
     # partial slots: contiguous per split request, unique
     slots = segs[segs[:, 3] >= 0, 3]
     assert len(set(slots.tolist())) == len(slots) == plan.num_partials
