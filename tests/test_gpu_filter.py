@@ -144,3 +144,32 @@ def test_repeated_calls_reuse_workspace():
                                                        uniforms=u.to(DEV), top_k=tk, top_p=tp)
         for a, r in zip(got, ref):
             np.testing.assert_array_equal(a.cpu().numpy(), r)
+
+
+def test_randomized_filtered_chains():
+    """40 random cases (dtype, one-hot or draft logits, B, k, V, T, top_k, top_p, value
+    scale, quantisation for ties), bit-exact against the oracle."""
+    say("filtered chain: 40 randomized cases")
+    rng = np.random.default_rng(2024)
+    for case in range(40):
+        dt = ["bf16", "fp16", "fp32"][int(rng.integers(3))]
+        onehot = bool(rng.random() < 0.4)
+        B = int(rng.integers(1, 7))
+        k = int(rng.integers(0, 5))
+        V = int(rng.choice([17, 255, 1000, 4099, 9000, 20000]))
+        T = float(rng.choice([0.3, 0.6, 1.0, 1.7]))
+        top_k = int(rng.choice([0, 1, 3, 20, 64, 300, V - 1, V + 5]))
+        top_p = float(rng.choice([0.0, 0.3, 0.8, 0.95, 0.999, 1.0]))
+        sigma = float(rng.choice([0.2, 2.0, 6.0]))
+        q = None if rng.random() < 0.7 else float(rng.choice([1.0, 4.0]))
+        t, d, ids, u = _case(B, k, V, DT[dt], T, top_k, top_p, seed=int(rng.integers(1 << 30)),
+                             sigma=sigma, quantize=q, draft_from="argmax" if onehot else "filtered")
+        ref = OAc.chain_filtered(None if onehot else d.float().numpy(), ids.numpy(),
+                                 t.float().numpy(), T, top_k, top_p, u.numpy())
+        got = S.chain_speculative_sampling_from_logits(None if onehot else d.to(DEV), ids.to(DEV),
+                                                       t.to(DEV), T, uniforms=u.to(DEV),
+                                                       top_k=top_k, top_p=top_p)
+        for a, r in zip(got, ref):
+            np.testing.assert_array_equal(a.cpu().numpy(), r, err_msg=f"case {case}: {dt} onehot="
+                                          f"{onehot} B={B} k={k} V={V} T={T} top_k={top_k} "
+                                          f"top_p={top_p} sigma={sigma} q={q}")
