@@ -65,6 +65,8 @@ class AttnPlan(ctypes.Structure):
         ("safe_page_pos", c_int32),
         ("shared_kv_tiles", c_int32),
         ("total_tiles", c_int64),
+        ("device_plan", c_int32),
+        ("off_dyn", c_int32),
     ]
 
 
@@ -78,6 +80,9 @@ SIGNATURES = {
     "bsx_attn_plan_ints_bound": (c_int64, [c_int, c_int]),
     "bsx_attn_plan": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                               c_float, c_int, _P, c_int64, POINTER(AttnPlan)]),
+    "bsx_attn_plan_device_shape": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                           c_float, c_int, c_int, POINTER(AttnPlan)]),
+    "bsx_attn_plan_device": (c_int, [POINTER(AttnPlan), _P, _P, _P, _P, _P]),
     "bsx_attn_run": (c_int, [POINTER(AttnPlan), _P, _P, c_int, _P, c_int64, _P, _P, c_int64, _P,
                              _P, _P, c_int64, _P, _P]),
     "bsx_get_seq_lens": (c_int, [_P, _P, c_int, c_int, _P, _P]),

@@ -119,12 +119,22 @@ class BatchPrefillWithPagedKVCacheWrapper:
              rope_theta: Optional[float] = None, q_data_type: Union[str, torch.dtype] = "float16",
              kv_data_type: Union[str, torch.dtype, None] = None, non_blocking: bool = True,
              *, tree_mask_words: Optional[torch.Tensor] = None, sink_tokens: int = 0,
-             window_tokens: int = 0) -> None:
+             window_tokens: int = 0, on_device: bool = False,
+             max_qo_len: Optional[int] = None) -> None:
         """Schedule one step of attention; shared by every layer until the next plan.
 
         Mirrors FlashInfer's plan (arguments as passed at
         batchspec/backends/standard_engine.py:132-143).  Host-synchronising: the
         indptr arrays are read on the host, as FlashInfer does.
+
+        With ``on_device=True`` (no counterpart in the reference) the schedule is
+        computed on the GPU from the device tensors, stream-ordered and without a host
+        synchronisation, so plan() and run() can be captured in one graph and replayed
+        with page-table lengths that change between replays.  ``max_qo_len`` bounds
+        every request's query tokens; q and out then need ``batch * max_qo_len`` token
+        rows.  Masks: causal, sink+window, or ``tree_mask_words`` (device tensor, one
+        word per token row); a boolean ``custom_mask`` needs the host path.
+        Malformed tables are reported by :meth:`device_plan_error`, not raised.
         """
         if head_dim_vo is not None and head_dim_vo != head_dim_qk:
             raise NotImplementedError("head_dim_vo != head_dim_qk")
@@ -142,6 +152,13 @@ class BatchPrefillWithPagedKVCacheWrapper:
         kdt = _as_dtype(kv_data_type) if kv_data_type is not None else qdt
         if kdt != qdt:
             raise NotImplementedError("kv_data_type must equal q_data_type")
+
+        if on_device:
+            self._plan_on_device(qo_indptr, paged_kv_indptr, paged_kv_indices,
+                                 paged_kv_last_page_len, num_qo_heads, num_kv_heads, head_dim_qk,
+                                 page_size, custom_mask, causal, sm_scale, qdt, tree_mask_words,
+                                 sink_tokens, window_tokens, max_qo_len, non_blocking)
+            return
 
         qo_h = _host_i32(qo_indptr)
         kvp_h = _host_i32(paged_kv_indptr)
@@ -214,6 +231,13 @@ class BatchPrefillWithPagedKVCacheWrapper:
                 self._copy_done = torch.cuda.Event()
             self._copy_done.record()
 
+        self._set_kv_indices(paged_kv_indices, non_blocking)
+        if words is not None:
+            self._set_mask_words(words, int(plan.total_qo))
+        self._plan = plan
+        self._dtype = qdt
+
+    def _set_kv_indices(self, paged_kv_indices: torch.Tensor, non_blocking: bool) -> None:
         # Page ids: in graph mode run() reads the registered buffer.
         if self._use_cuda_graph:
             nidx = paged_kv_indices.numel()
@@ -228,25 +252,87 @@ class BatchPrefillWithPagedKVCacheWrapper:
         if self._kv_indices.dtype != torch.int32:
             raise ValueError("paged_kv_indices must be int32")
 
-        if words is not None:
-            if isinstance(words, torch.Tensor):
-                w = words.to(torch.int32)
-            else:
-                w = torch.from_numpy(np.ascontiguousarray(
-                    np.asarray(words, dtype=np.uint32).view(np.int32)))
-            if w.numel() < int(plan.total_qo):
-                raise ValueError("tree_mask_words needs one word per query token")
-            w = w.reshape(-1)[: int(plan.total_qo)]
-            if self._mask_words is None or self._mask_words.numel() < w.numel():
-                if self._use_cuda_graph and self._mask_words is not None:
-                    raise ValueError("mask grew beyond its cuda-graph buffer")
-                cap = max(w.numel(), 1)
-                if self._use_cuda_graph and self._qo_indptr_buf is not None:
-                    cap = max(cap, 32 * (self._qo_indptr_buf.numel()))
-                self._mask_words = torch.zeros(cap, dtype=torch.int32, device=self._device)
-            self._mask_words[: w.numel()].copy_(w, non_blocking=True)
+    def _set_mask_words(self, words, rows: int) -> None:
+        if isinstance(words, torch.Tensor):
+            w = words.view(torch.int32) if words.dtype in (torch.int32, torch.uint32) \
+                else words.to(torch.int32)
+        else:
+            w = torch.from_numpy(np.ascontiguousarray(
+                np.asarray(words, dtype=np.uint32).view(np.int32)))
+        if w.numel() < rows:
+            raise ValueError("tree_mask_words needs one word per query token")
+        w = w.reshape(-1)[:rows]
+        if self._mask_words is None or self._mask_words.numel() < w.numel():
+            if self._use_cuda_graph and self._mask_words is not None:
+                raise ValueError("mask grew beyond its cuda-graph buffer")
+            cap = max(w.numel(), 1)
+            if self._use_cuda_graph and self._qo_indptr_buf is not None:
+                cap = max(cap, 32 * (self._qo_indptr_buf.numel()))
+            self._mask_words = torch.zeros(cap, dtype=torch.int32, device=self._device)
+        self._mask_words[: w.numel()].copy_(w, non_blocking=True)
+
+    def _plan_on_device(self, qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len,
+                        num_qo_heads, num_kv_heads, head_dim, page_size, custom_mask, causal,
+                        sm_scale, qdt, tree_mask_words, sink_tokens, window_tokens, max_qo_len,
+                        non_blocking) -> None:
+        if max_qo_len is None or int(max_qo_len) < 1:
+            raise ValueError("plan(on_device=True) needs max_qo_len >= 1")
+        if custom_mask is not None:
+            raise NotImplementedError("plan(on_device=True) takes tree_mask_words, not custom_mask")
+        streaming = sink_tokens > 0 or window_tokens > 0
+        if tree_mask_words is not None:
+            if causal or streaming:
+                raise ValueError("tree mask cannot be combined with causal or streaming")
+            mode = _lib.MASK_TREE
+        elif streaming:
+            mode = _lib.MASK_STREAMING
+        elif causal:
+            mode = _lib.MASK_CAUSAL
+        else:
+            mode = _lib.MASK_NONE
+        dev = require_gpu("plan", qo_indptr, paged_kv_indptr, paged_kv_last_page_len)
+        batch = qo_indptr.numel() - 1
+        if batch < 1 or paged_kv_indptr.numel() != batch + 1 \
+                or paged_kv_last_page_len.numel() < batch:
+            raise ValueError("qo_indptr, paged_kv_indptr and paged_kv_last_page_len disagree on batch")
+        lib = _lib.load()
+        plan = _lib.AttnPlan()
+        rc = lib.bsx_attn_plan_device_shape(batch, int(num_qo_heads), int(num_kv_heads),
+                                            int(head_dim), int(page_size), mode, int(sink_tokens),
+                                            int(window_tokens),
+                                            float(sm_scale) if sm_scale else 0.0, self._num_cus,
+                                            int(max_qo_len), ctypes.byref(plan))
+        _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan(on_device=True)")
+        blob_bytes = _align(int(plan.plan_ints) * 4)
+        if self._use_cuda_graph:
+            blob_bytes = max(self._blob_bytes, blob_bytes)
+        need = blob_bytes + int(plan.float_ws_bytes)
+        if need > self._ws.numel():
+            raise ValueError(f"float_workspace_buffer too small: need {need} bytes, "
+                             f"have {self._ws.numel()}")
+        self._blob_bytes = blob_bytes
+        self._dev_idx = [t if t.dtype == torch.int32 and t.is_contiguous()
+                         else t.to(torch.int32).contiguous()
+                         for t in (qo_indptr, paged_kv_indptr, paged_kv_last_page_len)]
+        blob = self._ws[: int(plan.plan_ints) * 4]
+        rc = lib.bsx_attn_plan_device(ctypes.byref(plan), self._dev_idx[0].data_ptr(),
+                                      self._dev_idx[1].data_ptr(), self._dev_idx[2].data_ptr(),
+                                      blob.data_ptr(), stream_of(dev))
+        _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan(on_device=True)")
+        self._set_kv_indices(paged_kv_indices, non_blocking)
+        if tree_mask_words is not None:
+            self._set_mask_words(tree_mask_words, int(plan.total_qo))
         self._plan = plan
         self._dtype = qdt
+
+    def device_plan_error(self) -> int:
+        """Error code the device planner left for the last plan(on_device=True) (0: none;
+        reads device memory, so it synchronises)."""
+        plan = self._plan
+        if plan is None or not plan.device_plan:
+            return 0
+        return int(self._ws[int(plan.off_dyn) * 4: int(plan.off_dyn) * 4 + 8]
+                   .view(torch.int32)[1].item())
 
     # ------------------------------------------------------------------- run
     def run(self, q: torch.Tensor,
@@ -262,20 +348,20 @@ class BatchPrefillWithPagedKVCacheWrapper:
         if q.dtype != k_cache.dtype or q.dtype not in (torch.bfloat16, torch.float16):
             raise ValueError(f"q ({q.dtype}) and paged_kv_cache ({k_cache.dtype}) must both be "
                              "bf16 or fp16")
-        if q.dim() != 3 or tuple(q.shape[1:]) != (plan.num_qo_heads, plan.head_dim) \
-                or q.shape[0] != plan.total_qo:
+        rows_ok = q.shape[0] >= plan.total_qo if plan.device_plan else q.shape[0] == plan.total_qo
+        if q.dim() != 3 or tuple(q.shape[1:]) != (plan.num_qo_heads, plan.head_dim) or not rows_ok:
             raise ValueError(f"q shape {tuple(q.shape)} does not match the plan "
                              f"[{plan.total_qo}, {plan.num_qo_heads}, {plan.head_dim}]")
         if q.stride(2) != 1 or q.stride(1) != plan.head_dim:
             q = q.contiguous()
         if out is None:
-            out = torch.empty((plan.total_qo, plan.num_qo_heads, plan.head_dim), dtype=q.dtype,
-                              device=dev)
+            out = torch.empty_like(q) if plan.device_plan else torch.empty(
+                (plan.total_qo, plan.num_qo_heads, plan.head_dim), dtype=q.dtype, device=dev)
         elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 \
                 or out.stride(1) != plan.head_dim:
             raise ValueError("out must match q in shape and dtype with dense heads")
         if return_lse and lse is None:
-            lse = torch.empty((plan.total_qo, plan.num_qo_heads), dtype=torch.float32, device=dev)
+            lse = torch.empty((q.shape[0], plan.num_qo_heads), dtype=torch.float32, device=dev)
         if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()):
             raise ValueError("lse must be a contiguous float32 tensor")
         ws = self._ws

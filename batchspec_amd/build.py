@@ -40,6 +40,7 @@ HIP_SOURCES = {
     "collate.hip": [],
     "masks.hip": [],
     "page_table.hip": [],
+    "plan_device.hip": [],
     "accept.hip": ["-ffp-contract=off"],
     "filter.hip": ["-ffp-contract=off"],
 }

@@ -48,6 +48,7 @@ struct Params {
   const int32_t* blob;
   int off_seq, off_seg_indptr, off_segments, off_merge_seqs, off_part_indptr;
   int safe_pos;  // a valid position in kv_indices (used for loads of empty requests)
+  int off_dyn;   // device plans: blob offset of {split requests, ...}; -1 otherwise
   const uint16_t* q;
   int64_t q_stride;  // elements between tokens
   const char* k_cache;
@@ -954,6 +955,8 @@ __global__ void __launch_bounds__(256) merge_kernel(Params p) {
   // the request's merge record {first part, end of parts, first query token, query
   // tokens}: one scalar load
   typedef const u32x4 __attribute__((address_space(4)))* const_u4_ptr;
+  // (a device plan's grid covers every request; its record count is in the blob)
+  if (p.off_dyn >= 0 && (int)blockIdx.x >= ld_uniform(p.blob, p.off_dyn)) return;
   const u32x4 rec = ((const_u4_ptr)(p.blob + p.off_merge_seqs))[blockIdx.x];
   const int h = blockIdx.y;
   const int pbeg = (int)rec[0];
@@ -1122,6 +1125,7 @@ extern "C" int bsx_attn_run(const bsx_attn_plan_t* plan, const int32_t* plan_blo
   prm.off_segments = plan->off_segments;
   prm.off_part_indptr = plan->off_part_indptr;
   prm.safe_pos = plan->safe_page_pos;
+  prm.off_dyn = plan->device_plan ? plan->off_dyn : -1;
   prm.q = static_cast<const uint16_t*>(q_d);
   prm.q_stride = q_stride_tok;
   prm.k_cache = static_cast<const char*>(k_cache_d);

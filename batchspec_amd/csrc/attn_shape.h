@@ -6,6 +6,14 @@ namespace bsx {
 namespace attn_shape {
 
 constexpr int kTileTokens = 32;     // kv tokens per inner-loop tile
+// Planner cost of starting a segment, in kv tiles: the Q load of the new request (one
+// memory latency) and the write of its (partial) result, measured on MI355X at about
+// two tile times together.
+constexpr int kSegmentCost = 2;
+// Largest batch and grid a device-side plan handles (its per-request and
+// per-segment state lives in LDS).
+constexpr int kMaxDevicePlanBatch = 2048;
+constexpr int kMaxDevicePlanCtas = 4096;
 constexpr int kMaxWavesPerCta = 8;
 constexpr int kLdsPerCu = 160 * 1024;
 

@@ -42,10 +42,7 @@ namespace {
 
 using bsx::attn_shape::kMaxWavesPerCta;
 using bsx::attn_shape::kTileTokens;
-// Cost of starting a segment, in kv tiles: the Q load of the new request (one memory
-// latency) and the write of its (partial) result, measured on MI355X at about two
-// tile times together.
-constexpr int64_t kSegmentCost = 2;
+constexpr int64_t kSegmentCost = bsx::attn_shape::kSegmentCost;
 
 struct Unit {
   int b;
@@ -95,6 +92,52 @@ int64_t pack_units(const std::vector<Unit>& units, int64_t cap, int64_t max_ctas
 static int waves_per_simd(int head_dim, int qrow_tile) {
   if (head_dim == 128) return 2;
   return qrow_tile == 16 ? 4 : 3;
+}
+
+// Workgroup shape and persistent grid of the attention kernels for query rows per kv
+// head of up to max_qo * group (shared by the host and the device planner).
+struct GridShape {
+  int qrow_tile, qrow_blocks, hpc, qbpc, n_qgroups, num_ctas;
+  bool shared;
+};
+
+static GridShape grid_shape(int max_qo, int group, int num_kv_heads, int head_dim, int page_size,
+                     int num_cus) {
+  GridShape g;
+  // Query rows per kv head = qo_len * group.  A wave covers 16 or 32 of them.
+  const int64_t max_rows = (int64_t)max_qo * group;
+  g.qrow_tile = max_rows <= 16 ? 16 : 32;
+  g.qrow_blocks = (int)std::max<int64_t>(1, (max_rows + g.qrow_tile - 1) / g.qrow_tile);
+  // Several waves per kv head: they share each K/V tile through LDS when a 16-token
+  // subtile always lies inside one page (the shared kernel's loads assume it).
+  g.shared = g.qrow_blocks > 1 && page_size >= 16;
+  g.hpc = 1;  // kv heads per workgroup: largest divisor of num_kv_heads that fits
+  if (g.shared) {
+    g.qbpc = g.qrow_blocks <= 2 ? 2 : g.qrow_blocks <= 4 ? 4 : 8;
+    for (int c = 1; c <= num_kv_heads; ++c)
+      if (num_kv_heads % c == 0 && c <= bsx::attn_shape::shared_max_heads(head_dim, g.qbpc))
+        g.hpc = c;
+  } else {
+    for (int c = 1; c <= num_kv_heads; ++c)
+      if (num_kv_heads % c == 0 &&
+          c * std::min(g.qrow_blocks, kMaxWavesPerCta) <= kMaxWavesPerCta)
+        g.hpc = c;
+    g.qbpc = g.qrow_blocks;
+    while (g.qbpc * g.hpc > kMaxWavesPerCta) g.qbpc = (g.qbpc + 1) / 2;
+  }
+  g.n_qgroups = (g.qrow_blocks + g.qbpc - 1) / g.qbpc;
+  const int cta_waves = g.hpc * g.qbpc;
+  // One grid row (blockIdx.y) per (kv-head group, query group); size grid.x so that
+  // all workgroups are resident at once on num_cus compute units (4 SIMDs each; the
+  // shared kernel's LDS ring also bounds its workgroups per compute unit).
+  const int grid_y = (num_kv_heads / g.hpc) * g.n_qgroups;
+  int resident_per_cu = std::max(1, 4 * waves_per_simd(head_dim, g.qrow_tile) / cta_waves);
+  if (g.shared)
+    resident_per_cu = std::max(
+        1, std::min(resident_per_cu, bsx::attn_shape::kLdsPerCu /
+                                         bsx::attn_shape::shared_lds_bytes(head_dim, g.qbpc)));
+  g.num_ctas = std::max(1, (num_cus * resident_per_cu) / grid_y);
+  return g;
 }
 
 extern "C" int64_t bsx_attn_plan_ints_bound(int batch, int num_cus) {
@@ -154,39 +197,11 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
     max_qo = std::max(max_qo, q);
   }
 
-  // Query rows per kv head = qo_len * group.  A wave covers 16 or 32 of them.
-  const int64_t max_rows = (int64_t)max_qo * group;
-  const int qrow_tile = max_rows <= 16 ? 16 : 32;
-  const int qrow_blocks = (int)std::max<int64_t>(1, (max_rows + qrow_tile - 1) / qrow_tile);
-  // Several waves per kv head: they share each K/V tile through LDS when a 16-token
-  // subtile always lies inside one page (the shared kernel's loads assume it).
-  const bool shared = qrow_blocks > 1 && page_size >= 16;
-  int hpc = 1;  // kv heads per workgroup: largest divisor of num_kv_heads that fits
-  int qbpc;     // query blocks (waves) per kv head in one workgroup
-  if (shared) {
-    qbpc = qrow_blocks <= 2 ? 2 : qrow_blocks <= 4 ? 4 : 8;
-    for (int c = 1; c <= num_kv_heads; ++c)
-      if (num_kv_heads % c == 0 && c <= bsx::attn_shape::shared_max_heads(head_dim, qbpc))
-        hpc = c;
-  } else {
-    for (int c = 1; c <= num_kv_heads; ++c)
-      if (num_kv_heads % c == 0 && c * std::min(qrow_blocks, kMaxWavesPerCta) <= kMaxWavesPerCta)
-        hpc = c;
-    qbpc = qrow_blocks;
-    while (qbpc * hpc > kMaxWavesPerCta) qbpc = (qbpc + 1) / 2;
-  }
-  const int n_qgroups = (qrow_blocks + qbpc - 1) / qbpc;
-  const int cta_waves = hpc * qbpc;
-  // One grid row (blockIdx.y) per (kv-head group, query group); size grid.x so that
-  // all workgroups are resident at once on num_cus compute units (4 SIMDs each; the
-  // shared kernel's LDS ring also bounds its workgroups per compute unit).
-  const int grid_y = (num_kv_heads / hpc) * n_qgroups;
-  int resident_per_cu = std::max(1, 4 * waves_per_simd(head_dim, qrow_tile) / cta_waves);
-  if (shared)
-    resident_per_cu = std::max(
-        1, std::min(resident_per_cu,
-                    bsx::attn_shape::kLdsPerCu / bsx::attn_shape::shared_lds_bytes(head_dim, qbpc)));
-  const int num_ctas = std::max(1, (num_cus * resident_per_cu) / grid_y);
+  const GridShape gs = grid_shape(max_qo, group, num_kv_heads, head_dim, page_size, num_cus);
+  const int qrow_tile = gs.qrow_tile, qrow_blocks = gs.qrow_blocks, hpc = gs.hpc, qbpc = gs.qbpc;
+  const int n_qgroups = gs.n_qgroups;
+  const bool shared = gs.shared;
+  const int num_ctas = gs.num_ctas;
 
   // Work units: contiguous tile ranges per request (two for the sink+window view).
   std::vector<Unit> units;
@@ -323,5 +338,83 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   out->safe_page_pos = safe_pos;
   out->total_tiles = total_tiles;
   out->shared_kv_tiles = shared ? 1 : 0;
+  return BSX_OK;
+}
+
+// Device-planned attention: shape, grid and a blob layout sized by bounds (the
+// device planner, plan_device.hip, fills the blob from the device page table).
+extern "C" int bsx_attn_plan_device_shape(int batch, int num_qo_heads, int num_kv_heads,
+                                          int head_dim, int page_size, int mask_mode,
+                                          int sink_tokens, int window_tokens, float sm_scale,
+                                          int num_cus, int max_qo_len, bsx_attn_plan_t* out) {
+  PLAN_REQUIRE(out, BSX_ERR_INVALID, "null plan");
+  PLAN_REQUIRE(batch >= 1 && batch <= bsx::attn_shape::kMaxDevicePlanBatch, BSX_ERR_UNSUPPORTED,
+               "device plans take 1..%d requests (got %d)", bsx::attn_shape::kMaxDevicePlanBatch,
+               batch);
+  PLAN_REQUIRE(num_kv_heads > 0 && num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0,
+               BSX_ERR_INVALID, "num_qo_heads (%d) must be a positive multiple of num_kv_heads (%d)",
+               num_qo_heads, num_kv_heads);
+  PLAN_REQUIRE(head_dim == 64 || head_dim == 128, BSX_ERR_UNSUPPORTED,
+               "head_dim %d not supported (64 or 128)", head_dim);
+  PLAN_REQUIRE(page_size >= 1 && page_size <= 1024 && (page_size & (page_size - 1)) == 0,
+               BSX_ERR_UNSUPPORTED, "page_size %d must be a power of two <= 1024", page_size);
+  PLAN_REQUIRE(mask_mode >= BSX_MASK_NONE && mask_mode <= BSX_MASK_STREAMING, BSX_ERR_INVALID,
+               "unknown mask mode %d", mask_mode);
+  PLAN_REQUIRE(num_cus >= 1, BSX_ERR_INVALID, "num_cus must be >= 1");
+  PLAN_REQUIRE(mask_mode != BSX_MASK_STREAMING || (sink_tokens >= 0 && window_tokens >= 0),
+               BSX_ERR_INVALID, "streaming view needs sink >= 0 and window >= 0");
+  PLAN_REQUIRE(max_qo_len >= 1, BSX_ERR_INVALID, "max_qo_len must be >= 1");
+  PLAN_REQUIRE(mask_mode != BSX_MASK_TREE || max_qo_len <= 32, BSX_ERR_UNSUPPORTED,
+               "tree mask supports at most 32 query tokens per request");
+  const int group = num_qo_heads / num_kv_heads;
+  const GridShape gs = grid_shape(max_qo_len, group, num_kv_heads, head_dim, page_size, num_cus);
+  const int W = gs.num_ctas;
+  PLAN_REQUIRE(W <= bsx::attn_shape::kMaxDevicePlanCtas, BSX_ERR_UNSUPPORTED,
+               "grid of %d workgroups too large for a device plan", W);
+  const int64_t max_segs = (int64_t)W + 2LL * batch;
+  const int64_t off_seg_indptr = 4LL * batch;
+  const int64_t off_segments = off_seg_indptr + W + 1;
+  const int64_t off_merge = (off_segments + 4 * max_segs + 3) & ~3LL;
+  const int64_t off_part = off_merge + 4LL * batch;
+  const int64_t off_dyn = off_part + batch + 1;
+  const int64_t ints = off_dyn + 4;
+  PLAN_REQUIRE(ints < (1LL << 31), BSX_ERR_UNSUPPORTED, "batch too large for a device plan");
+
+  memset(out, 0, sizeof(*out));
+  out->batch = batch;
+  out->num_qo_heads = num_qo_heads;
+  out->num_kv_heads = num_kv_heads;
+  out->head_dim = head_dim;
+  out->page_size = page_size;
+  out->mask_mode = mask_mode;
+  out->group_size = group;
+  out->qrow_tile = gs.qrow_tile;
+  out->qrow_blocks = gs.qrow_blocks;
+  out->heads_per_cta = gs.hpc;
+  out->qblocks_per_cta = gs.qbpc;
+  out->num_qgroups = gs.n_qgroups;
+  out->num_ctas = W;
+  out->num_segments = (int32_t)max_segs;
+  out->num_partials = (int32_t)max_segs;
+  out->num_split_requests = batch;  // bound: the merge grid covers every request
+  out->max_qo_len = max_qo_len;
+  out->tile_tokens = kTileTokens;
+  out->sink_tokens = sink_tokens;
+  out->window_tokens = window_tokens;
+  out->off_seq = 0;
+  out->off_seg_indptr = (int32_t)off_seg_indptr;
+  out->off_segments = (int32_t)off_segments;
+  out->off_merge_seqs = (int32_t)off_merge;
+  out->off_part_indptr = (int32_t)off_part;
+  out->plan_ints = (int32_t)ints;
+  const int64_t rows_total = (int64_t)gs.qrow_tile * gs.qrow_blocks;
+  out->float_ws_bytes = max_segs * num_kv_heads * rows_total * (head_dim * 2 + 4);
+  out->sm_scale = sm_scale > 0.f ? sm_scale : 1.0f / std::sqrt((float)head_dim);
+  out->total_qo = batch * max_qo_len;  // bound: q / out need this many token rows
+  out->safe_page_pos = 0;  // the table holds a page (checked by the planner)
+  out->shared_kv_tiles = gs.shared ? 1 : 0;
+  out->total_tiles = -1;
+  out->device_plan = 1;
+  out->off_dyn = (int32_t)off_dyn;
   return BSX_OK;
 }

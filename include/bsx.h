@@ -101,6 +101,10 @@ typedef struct {
                              each K/V tile through LDS (many query rows per
                              kv head); 0: every wave streams its own tiles   */
   int64_t total_tiles;    /* kv tiles of the whole schedule                   */
+  int32_t device_plan;    /* 1: the blob is written on the device by
+                             bsx_attn_plan_device; counts above are bounds    */
+  int32_t off_dyn;        /* device plan: int32 offset of {split requests,
+                             error code, segments, reserved} in the blob      */
 } bsx_attn_plan_t;
 
 /* Size (int32 entries) of the host buffer bsx_attn_plan needs for its blob. */
@@ -121,6 +125,34 @@ int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
                   int sink_tokens, int window_tokens, float sm_scale, int num_cus,
                   int32_t* plan_blob_h, int64_t blob_capacity_ints,
                   bsx_attn_plan_t* plan_out);
+
+/* Device-side planning (no counterpart in the reference, whose plan() always
+ * schedules on the host from host copies of the page table,
+ * batchspec/backends/base/attn_wrapper.py:33-72 with the callers above): the
+ * schedule is computed by one GPU workgroup from the device page table, so a verify
+ * step (page-table update, plan, attention, acceptance) can be captured in one graph
+ * and replayed with lengths that change between replays.
+ *
+ * bsx_attn_plan_device_shape (host only) fixes what a graph needs to know at
+ * capture time: the workgroup shape for query lengths up to max_qo_len, the grid,
+ * the blob layout and the float workspace, all sized by bounds for `batch`
+ * requests.  bsx_attn_plan_device (stream-ordered, no host synchronisation) then
+ * writes the blob from qo_indptr_d[batch+1], kv_indptr_d[batch+1] and
+ * kv_last_page_len_d[batch].  The device schedule cuts the kv tiles into equal
+ * cost shares of the fixed grid (a tile costs 1, a segment start 2, as in
+ * bsx_attn_plan).  Requirements checked on the device: indptrs non-decreasing from
+ * 0, last-page lengths in [0, page_size], query lengths at most max_qo_len (32 in
+ * tree mode), and at least one page in the table; a violation writes an error code
+ * (BSX_ERR_*) into blob[off_dyn + 1] and an empty schedule (no output is written),
+ * otherwise 0.  A device plan's total_qo is the bound batch * max_qo_len: q and out
+ * passed to bsx_attn_run need that many token rows. */
+int bsx_attn_plan_device_shape(int batch, int num_qo_heads, int num_kv_heads, int head_dim,
+                               int page_size, int mask_mode, int sink_tokens,
+                               int window_tokens, float sm_scale, int num_cus, int max_qo_len,
+                               bsx_attn_plan_t* plan_out);
+int bsx_attn_plan_device(const bsx_attn_plan_t* plan, const int32_t* qo_indptr_d,
+                         const int32_t* kv_indptr_d, const int32_t* kv_last_page_len_d,
+                         int32_t* plan_blob_d, void* stream);
 
 /* Replaces BatchPrefillWithPagedKVCacheWrapper.run(q, paged_kv_cache) as called
  * at batchspec/models/modules/attention/standard.py:69.
