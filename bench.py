@@ -188,6 +188,40 @@ def extra_configs(dev, iters: int):
     host_us = (time.perf_counter() - t0) / iters * 1e6
     out["page_table_step"] = {"device_us": round(sum(us) / len(us), 2),
                               "torch_mirror_wall_us": round(host_us, 1), "requests": 64}
+
+    # the device-side schedule at config 2 (one planner launch per step) and the
+    # attention pass run on it; the host planner's wall time for comparison
+    from batchspec_amd.workloads import config2
+    s2 = [config2(device=dev, seed=1002 + i) for i in range(3)]
+    ws2 = [bsx.BatchPrefillWithPagedKVCacheWrapper(torch.empty(256 << 20, dtype=torch.uint8,
+                                                               device=dev), "NHD") for _ in s2]
+    dev_args = [(b.qo_indptr.to(dev), b.kv_indptr.to(dev), b.kv_indices.to(dev),
+                 b.kv_last_page_len.to(dev)) for b in s2]
+
+    def plan_dev(i):
+        b = s2[i % 3]
+        ws2[i % 3].plan(*dev_args[i % 3], b.num_qo_heads, b.num_kv_heads, b.head_dim, b.page_size,
+                        causal=True, q_data_type=torch.bfloat16, on_device=True, max_qo_len=5)
+    plan_us = time_events(plan_dev, iters, 3)
+    outs2 = [torch.empty_like(b.q) for b in s2]
+    run_us = time_events(lambda i: ws2[i % 3].run(s2[i % 3].q, s2[i % 3].cache, out=outs2[i % 3]),
+                         iters, 3)
+    t = sum(run_us) / len(run_us)
+    nb = sum(attn_bytes(b) for b in s2) / 3
+    hw = bsx.BatchPrefillWithPagedKVCacheWrapper(torch.empty(256 << 20, dtype=torch.uint8,
+                                                             device=dev), "NHD")
+    t0 = time.perf_counter()
+    for i in range(iters):
+        b = s2[i % 3]
+        hw.plan(dev_args[i % 3][0], dev_args[i % 3][1], dev_args[i % 3][2], dev_args[i % 3][3],
+                b.num_qo_heads, b.num_kv_heads, b.head_dim, b.page_size, causal=True,
+                q_data_type=torch.bfloat16)
+    torch.cuda.synchronize()
+    host_plan_us = (time.perf_counter() - t0) / iters * 1e6
+    out["config2_device_plan"] = {"plan_kernel_us": round(sum(plan_us) / len(plan_us), 2),
+                                  "attention_us": round(t, 2),
+                                  "frac": round(nb / t / 1e3 / HBM_PEAK_GBS, 4),
+                                  "host_plan_wall_us": round(host_plan_us, 1)}
     return out
 
 
