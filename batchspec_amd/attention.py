@@ -106,6 +106,9 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._pinned: Optional[torch.Tensor] = None
         self._copy_done: Optional[torch.cuda.Event] = None
         self._dtype: Optional[torch.dtype] = None
+        # device plans: the int32 page-table tensors the planner reads (kept alive while
+        # a captured graph may replay them)
+        self._dev_idx: list = []
 
     # ------------------------------------------------------------------ plan
     def plan(self, qo_indptr: torch.Tensor, paged_kv_indptr: torch.Tensor,
