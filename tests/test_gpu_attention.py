@@ -115,6 +115,21 @@ def test_ragged_mixed_batch_with_empty_requests():
     check(out, oracle_out(b, "causal"))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_continuous_batching_mix(dtype):
+    """The continuous-batching scheduler's mix (batchspec/backends/continuous/scheduler.py:
+    189-204): prefill chunks up to 128 tokens, verify rows of k+1, decode rows and dummy
+    1-token slots in one plan; 128 tokens x GQA 4 = 512 query rows per kv head."""
+    say(f"continuous-batching mix: prefill chunks 128/64, verify 5, decode 1, {dtype}")
+    qo = np.array([128, 5, 5, 1, 1, 64, 5, 1])
+    ctx = np.array([0, 900, 2500, 4000, 0, 300, 17, 1])
+    b = make_verify_batch(8, 0, 0, 0, 32, 8, 128, 16, dtype=dtype, scale=0.5, seed=19,
+                          qo_lens=qo, ctx=ctx).to(DEV)
+    out, w = run_gpu(b)
+    assert w.plan_info.shared_kv_tiles == 1 and w.plan_info.num_qgroups == 2
+    check(out, oracle_out(b, "causal"))
+
+
 def test_non_causal():
     say("non-causal")
     b = make_verify_batch(5, 10, 500, 5, 32, 8, 128, 16, dtype=torch.bfloat16, seed=3).to(DEV)
