@@ -21,6 +21,11 @@ Printed: one JSON line with
   stochastic_accept  config 5 (B=128, k=5, V=128256, bf16): time and HBM fraction
   cpu_baseline    the fp32 CPU oracle on a bounded sample of the same workload
 
+`--extra-configs` adds verify attention at configs 4 (EAGLE trees), 3b (long context)
+and 3a (sink+window draft view), the device tree masks of config 4, one step of the
+sync-free page-table update at B=64 beside the host-synchronising torch mirror, and the
+device-side attention schedule at config 2 with the attention pass run on it.
+
 `--calibrate-copy` instead times a plain 1 GiB device copy (the known-size kernel
 the HBM byte counters are scaled against).
 """
