@@ -130,6 +130,29 @@ def test_continuous_batching_mix(dtype):
     check(out, oracle_out(b, "causal"))
 
 
+@pytest.mark.parametrize("ps", [1, 8])
+def test_many_query_rows_on_small_pages(ps):
+    """Pages under 16 tokens keep the per-wave kernel even with several query blocks per kv
+    head: 32-node trees (128 rows per kv head) and 16-token causal drafts (64 rows)."""
+    say(f"page size {ps}: 32-node trees, then 16-token causal drafts")
+    b = make_verify_batch(5, 40, 1500, 32, 32, 8, 128, ps, dtype=torch.bfloat16, scale=0.5,
+                          seed=40 + ps, tree_nodes=32).to(DEV)
+    out, w = run_gpu(b, causal=False, tree_mask_words=b.mask_words)
+    assert w.plan_info.shared_kv_tiles == 0 and w.plan_info.qrow_blocks == 4
+    qo = np.diff(b.qo_indptr.cpu().numpy())
+    flat = []
+    for r, L in enumerate(b.kv_lens):
+        wd = b.mask_words[b.qo_indptr[r].item(): b.qo_indptr[r + 1].item()]
+        blk = ((wd[:, None].astype(np.uint64) >> np.arange(qo[r], dtype=np.uint64)) & 1).astype(bool)
+        flat.append(np.concatenate([np.ones((qo[r], L - qo[r]), bool), blk], 1).ravel())
+    check(out, oracle_out(b, "custom", custom_mask=np.concatenate(flat)))
+    c = make_verify_batch(6, 10, 900, 16, 32, 8, 128, ps, dtype=torch.float16, scale=0.5,
+                          seed=50 + ps).to(DEV)
+    out, w = run_gpu(c)
+    assert w.plan_info.shared_kv_tiles == 0
+    check(out, oracle_out(c, "causal"))
+
+
 def test_non_causal():
     say("non-causal")
     b = make_verify_batch(5, 10, 500, 5, 32, 8, 128, 16, dtype=torch.bfloat16, seed=3).to(DEV)
