@@ -33,7 +33,8 @@ def test_schedule_restatement_invariants(seed):
     s = OS.schedule(qo, kvp, last, ps, mode, sink, window, 8, W)
     assert s["dyn"][1] == 0
     OS.check_invariants(s, qo, kvp, last, ps, mode, sink, window)
-    # shares are even: no workgroup takes more than ceil(T / W) + 1 tiles
+    # shares are even: no workgroup's tiles exceed the mean share by more than a tile plus
+    # the segment charges its share may hold
     segs, sp = s["segments"], s["seg_indptr"]
     loads = [int((segs[sp[w]:sp[w + 1], 2] - segs[sp[w]:sp[w + 1], 1]).sum()) for w in range(W)]
     total = sum(loads)
@@ -91,3 +92,19 @@ def test_device_shape_rejects():
                                           ctypes.byref(plan)) != 0  # tree > 32 tokens
     assert lib.bsx_attn_plan_device_shape(5000, 32, 8, 128, 16, 1, 0, 0, 0.0, 256, 5,
                                           ctypes.byref(plan)) != 0  # batch above the bound
+
+
+def test_device_plan_entry_rejects_bad_arguments():
+    """bsx_attn_plan_device checks its arguments before launching anything (no GPU needed
+    for these paths)."""
+    lib = _lib.load()
+    plan = _lib.AttnPlan()
+    buf = np.zeros(16, np.int32)
+    p = buf.ctypes.data
+    # a host plan (device_plan == 0) is refused
+    assert lib.bsx_attn_plan_device(ctypes.byref(plan), p, p, p, p, None) == -1
+    rc = lib.bsx_attn_plan_device_shape(4, 32, 8, 128, 16, 1, 0, 0, 0.0, 256, 5, ctypes.byref(plan))
+    assert rc == 0
+    # null device pointers are refused
+    assert lib.bsx_attn_plan_device(ctypes.byref(plan), None, p, p, p, None) == -1
+    assert lib.bsx_attn_plan_device(ctypes.byref(plan), p, p, p, None, None) == -1
