@@ -14,7 +14,7 @@ All compute runs in ``libbsx.so`` (hand-written HIP for gfx950, C ABI in
 from .attention import BatchPrefillWithPagedKVCacheWrapper
 from .page import (StandardKVCache, append_kv, append_paged_kv_cache,
                    get_batch_indices_positions, get_seq_lens)
-from .page_table import PageManager, PageTable
+from .page_table import DevicePageTable
 from .posterior import PosteriorMixin, evaluate_posterior
 from . import masks, sampling
 
@@ -25,8 +25,7 @@ __all__ = [
     "append_paged_kv_cache",
     "get_batch_indices_positions",
     "get_seq_lens",
-    "PageManager",
-    "PageTable",
+    "DevicePageTable",
     "PosteriorMixin",
     "evaluate_posterior",
     "masks",

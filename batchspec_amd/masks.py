@@ -6,7 +6,6 @@
   (g_i == g_j and 1 <= r_j <= r_i); position_ids[i] = g_i + r_i.
 * ``mtp_verify_custom_mask`` — the flattened per-request mask
   cat(ones(S, cachelen_b), common_mask) of mtp_engine.py:410-417.
-* ``interleave_mask_tokens`` — mtp_engine.py:210-247.
 * ``tree_mask_words`` — ancestor-or-self bit words of a draft tree given by a parent
   array (EAGLE-style verification), one uint32 per node, bit j = node j.
 * ``mtp_parents`` / ``tree_masks`` / ``MTPMaskMixin`` — the same words and the position
@@ -42,17 +41,6 @@ def mtp_verify_custom_mask(cachelens: Sequence[int], draft_length: int, device=N
     parts = [torch.cat((torch.ones((S, int(c)), dtype=torch.bool, device=device), common), dim=-1)
              .flatten() for c in cachelens]
     return torch.cat(parts) if parts else torch.zeros(0, dtype=torch.bool, device=device)
-
-
-def interleave_mask_tokens(input_ids: torch.Tensor, draft_length: int, mask_token_id: int,
-                           dtype: torch.dtype = torch.bfloat16) -> Tuple[torch.Tensor, torch.Tensor]:
-    B, L = input_ids.shape
-    D = draft_length
-    out = torch.full((B, L * (D + 1)), mask_token_id, dtype=input_ids.dtype, device=input_ids.device)
-    out.view(B, L, D + 1)[:, :, 0] = input_ids
-    gate = torch.ones((B, L * (D + 1)), dtype=dtype, device=input_ids.device)
-    gate.view(B, L, D + 1)[:, :, 0] = 0
-    return out, gate[..., None]
 
 
 def mask_to_words(mask: torch.Tensor) -> np.ndarray:

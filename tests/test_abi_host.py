@@ -14,7 +14,6 @@ import batchspec_amd as bsx
 from batchspec_amd import _lib, masks
 from batchspec_amd.attention import custom_mask_to_tree_words
 from oracle import masks as OM
-from oracle import paging as OP
 
 ROOT = Path(__file__).resolve().parents[1]
 
@@ -35,7 +34,7 @@ def test_library_exports_every_header_symbol(bsx):
 
 
 def _plan(qo, kvp, last, Hq=32, Hkv=8, D=128, ps=16, mode=_lib.MASK_CAUSAL, cus=256, sink=0,
-          window=0):
+          window=0, nidx=-1):
     L = _lib.load()
     qo, kvp, last = (np.ascontiguousarray(a, dtype=np.int32) for a in (qo, kvp, last))
     B = len(qo) - 1
@@ -43,7 +42,8 @@ def _plan(qo, kvp, last, Hq=32, Hkv=8, D=128, ps=16, mode=_lib.MASK_CAUSAL, cus=
     blob = np.zeros(bound, np.int32)
     plan = _lib.AttnPlan()
     rc = L.bsx_attn_plan(qo.ctypes.data, kvp.ctypes.data, last.ctypes.data, B, Hq, Hkv, D, ps, mode,
-                         sink, window, 0.0, cus, blob.ctypes.data, bound, ctypes.byref(plan))
+                         sink, window, 0.0, cus, nidx, blob.ctypes.data, bound,
+                         ctypes.byref(plan))
     _lib.check(rc, "plan")
     return plan, blob
 
@@ -136,46 +136,6 @@ def test_plan_rejects_bad_page_table():
         _plan([0, 5, 4], [0, 1, 2], [3, 3])
     with pytest.raises(NotImplementedError, match="tree mask"):
         _plan([0, 33], [0, 3], [16], mode=_lib.MASK_TREE)
-
-
-def test_page_table_mirror_matches_oracle():
-    rng = np.random.default_rng(7)
-    pt = bsx.PageTable(16, 4, 512, "cpu")
-    pt.clear_kv()
-    ref = OP.Pages(4, 512, 16)
-    ref.clear_kv()
-    for _ in range(150):
-        if rng.random() < 0.6:
-            d = rng.integers(0, 40, size=4)
-            pt.insert_kv(torch.from_numpy(d.astype(np.int32)))
-            ref.insert_kv(d)
-        else:
-            tot = np.array([ref.total(r) for r in range(4)])
-            d = np.minimum(rng.integers(0, 30, size=4), tot)
-            pt.delete_kv(torch.from_numpy(d.astype(np.int32)))
-            ref.delete_kv(d)
-        indptr, indices, last = ref.table()
-        np.testing.assert_array_equal(pt.paged_kv_indptr.numpy(), indptr)
-        np.testing.assert_array_equal(pt.paged_kv_indices.numpy(), indices)
-        np.testing.assert_array_equal(pt.paged_kv_last_page_len.numpy(), last)
-
-
-def test_page_manager_mirror_known_answers_and_errors():
-    pm = bsx.PageManager(2, 64, "cpu")
-    ids = pm.allocate(torch.tensor([1, 1], dtype=torch.int32))
-    assert ids.tolist() == [0, 64]
-    indptr, indices = pm.allocate(torch.tensor([1, 0], dtype=torch.int32),
-                                  torch.tensor([0, 64], dtype=torch.int32),
-                                  torch.tensor([0, 1, 2], dtype=torch.int32))
-    assert indptr.tolist() == [0, 2, 3] and indices.tolist() == [0, 1, 64]
-    indptr, indices = pm.free(torch.tensor([1, 0], dtype=torch.int32), indices, indptr)
-    assert indptr.tolist() == [0, 1, 2] and indices.tolist() == [0, 64]
-    with pytest.raises(RuntimeError):
-        pm.free(torch.tensor([0, 5], dtype=torch.int32), indices, indptr)
-    small = bsx.PageManager(1, 1, "cpu")
-    small.allocate(torch.tensor([1], dtype=torch.int32))
-    with pytest.raises(RuntimeError):
-        small.allocate(torch.tensor([1], dtype=torch.int32))
 
 
 @pytest.mark.parametrize("k", [1, 2, 4])
