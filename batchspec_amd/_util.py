@@ -47,13 +47,21 @@ def num_cus(device_index: int) -> int:
 
 def workspace(device: torch.device, nbytes: int, cache: dict | None = None,
               key: str = "ws") -> torch.Tensor:
-    """A uint8 device buffer of at least `nbytes`, reused through `cache`."""
+    """A uint8 device buffer of at least `nbytes`, reused through `cache`.
+
+    A buffer that is outgrown is never freed: a graph captured while it was current
+    holds its address as a kernel argument, and replaying that graph must not write
+    into memory the caching allocator has handed to another tensor.  Growth doubles,
+    so the retired buffers together stay below the current one."""
     nbytes = max(int(nbytes), 256)
-    if cache is not None:
-        buf = cache.get(key)
-        if buf is not None and buf.numel() >= nbytes and buf.device == device:
-            return buf
+    if cache is None:
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    buf = cache.get(key)
+    if buf is not None and buf.numel() >= nbytes and buf.device == device:
+        return buf
+    if buf is not None:
+        cache.setdefault("__retired__", []).append(buf)
+        nbytes = max(nbytes, 2 * buf.numel())
     buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
-    if cache is not None:
-        cache[key] = buf
+    cache[key] = buf
     return buf
