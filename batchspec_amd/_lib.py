@@ -79,10 +79,12 @@ SIGNATURES = {
     "bsx_version": (c_int, []),
     "bsx_attn_plan_ints_bound": (c_int64, [c_int, c_int]),
     "bsx_attn_plan": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
-                              c_float, c_int, _P, c_int64, POINTER(AttnPlan)]),
+                              c_float, c_int, c_int64, _P, c_int64, POINTER(AttnPlan)]),
+    "bsx_attn_plan_fixed": (c_int, [POINTER(AttnPlan), _P, _P, _P, c_int, c_int64, _P, c_int64,
+                                    POINTER(AttnPlan)]),
     "bsx_attn_plan_device_shape": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                            c_float, c_int, c_int, POINTER(AttnPlan)]),
-    "bsx_attn_plan_device": (c_int, [POINTER(AttnPlan), _P, _P, _P, _P, _P]),
+    "bsx_attn_plan_device": (c_int, [POINTER(AttnPlan), _P, _P, _P, c_int64, _P, _P]),
     "bsx_attn_run": (c_int, [POINTER(AttnPlan), _P, _P, c_int, _P, c_int64, _P, _P, c_int64, _P,
                              _P, _P, c_int64, _P, _P]),
     "bsx_get_seq_lens": (c_int, [_P, _P, c_int, c_int, _P, _P]),

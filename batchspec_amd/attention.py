@@ -109,6 +109,12 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # device plans: the int32 page-table tensors the planner reads (kept alive while
         # a captured graph may replay them)
         self._dev_idx: list = []
+        # graph mode: the fixed shape every host plan is laid out in, and the launch
+        # arguments of the plan a captured run() replays (None until a capture)
+        self._graph_shape: Optional[_lib.AttnPlan] = None
+        self._graph_static: Optional[tuple] = None
+        self._captured_sig: Optional[tuple] = None
+        self._host_blob: Optional[np.ndarray] = None
 
     # ------------------------------------------------------------------ plan
     def plan(self, qo_indptr: torch.Tensor, paged_kv_indptr: torch.Tensor,
@@ -129,6 +135,13 @@ class BatchPrefillWithPagedKVCacheWrapper:
         Mirrors FlashInfer's plan (arguments as passed at
         batchspec/backends/standard_engine.py:132-143).  Host-synchronising: the
         indptr arrays are read on the host, as FlashInfer does.
+
+        With ``use_cuda_graph=True`` (how BatchSpec builds the wrapper,
+        batchspec/backends/base/attn_wrapper.py:53-57) the schedule is written into a
+        fixed, bound-sized layout (requests up to ``qo_indptr_buf``'s size, query tokens
+        per request up to the largest seen, or ``max_qo_len`` when given), so a graph
+        that captured run() replays every later plan of that shape.  A later plan that
+        needs a larger shape raises ValueError once a graph has captured run().
 
         With ``on_device=True`` (no counterpart in the reference) the schedule is
         computed on the GPU from the device tensors, stream-ordered and without a host
@@ -192,30 +205,43 @@ class BatchPrefillWithPagedKVCacheWrapper:
             mode = _lib.MASK_NONE
 
         lib = _lib.load()
-        bound = int(lib.bsx_attn_plan_ints_bound(batch, self._num_cus))
-        blob = np.empty(bound, dtype=np.int32)
+        nidx = int(paged_kv_indices.numel())
+        if int(kvp_h[-1]) > nidx:
+            raise ValueError(f"paged_kv_indptr[-1] = {int(kvp_h[-1])} exceeds the {nidx} entries "
+                             "of paged_kv_indices")
         plan = _lib.AttnPlan()
-        rc = lib.bsx_attn_plan(qo_h.ctypes.data, kvp_h.ctypes.data, last_h.ctypes.data, batch,
-                               int(num_qo_heads), int(num_kv_heads), int(head_dim_qk),
-                               int(page_size), mode, int(sink_tokens), int(window_tokens),
-                               float(sm_scale) if sm_scale else 0.0, self._num_cus,
-                               blob.ctypes.data, bound, ctypes.byref(plan))
-        _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan")
-
         if self._use_cuda_graph:
-            # the float region must not move between plans of a captured graph: size the
-            # blob region for the largest batch the registered buffers allow
-            max_batch = batch if self._qo_indptr_buf is None else max(
-                batch, self._qo_indptr_buf.numel() - 1)
-            region = _align(int(lib.bsx_attn_plan_ints_bound(max_batch, self._num_cus)) * 4)
-            blob_bytes = max(self._blob_bytes, region)
+            # FlashInfer's graph mode: plan() may be called again with other lengths and a
+            # graph that captured run() replays the new plan.  Every launch argument must
+            # therefore stay fixed: the schedule is laid out in a bound-sized shape.
+            static = (int(num_qo_heads), int(num_kv_heads), int(head_dim_qk), int(page_size),
+                      mode, int(sink_tokens), int(window_tokens), float(sm_scale or 0.0))
+            max_qo = int(np.diff(qo_h).max()) if batch > 0 else 0
+            shape = self._fixed_shape(lib, batch, max(max_qo, int(max_qo_len or 0)), static)
+            bound = int(shape.plan_ints)
+            blob = np.zeros(bound, dtype=np.int32)
+            rc = lib.bsx_attn_plan_fixed(ctypes.byref(shape), qo_h.ctypes.data, kvp_h.ctypes.data,
+                                         last_h.ctypes.data, batch, nidx, blob.ctypes.data, bound,
+                                         ctypes.byref(plan))
+            _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan")
+            blob_bytes = _align(bound * 4)
         else:
+            bound = int(lib.bsx_attn_plan_ints_bound(batch, self._num_cus))
+            blob = np.empty(bound, dtype=np.int32)
+            rc = lib.bsx_attn_plan(qo_h.ctypes.data, kvp_h.ctypes.data, last_h.ctypes.data, batch,
+                                   int(num_qo_heads), int(num_kv_heads), int(head_dim_qk),
+                                   int(page_size), mode, int(sink_tokens), int(window_tokens),
+                                   float(sm_scale) if sm_scale else 0.0, self._num_cus, nidx,
+                                   blob.ctypes.data, bound, ctypes.byref(plan))
+            _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan")
             blob_bytes = _align(bound * 4)
         need = blob_bytes + int(plan.float_ws_bytes)
         if need > self._ws.numel():
             raise ValueError(f"float_workspace_buffer too small: need {need} bytes, "
                              f"have {self._ws.numel()}")
+        self._check_captured(plan, blob_bytes)
         self._blob_bytes = blob_bytes
+        self._host_blob = blob[: int(plan.plan_ints)].copy()
 
         # Stage the blob through pinned memory; the previous copy must have landed
         # before its staging buffer is rewritten.
@@ -239,6 +265,47 @@ class BatchPrefillWithPagedKVCacheWrapper:
             self._set_mask_words(words, int(plan.total_qo))
         self._plan = plan
         self._dtype = qdt
+
+    def _fixed_shape(self, lib, batch: int, max_qo: int, static: tuple) -> _lib.AttnPlan:
+        """The bound-sized shape of graph mode: kept while plans fit it (same heads, page
+        size and mask; at most its requests and query tokens per request)."""
+        shp = self._graph_shape
+        if shp is not None and self._graph_static == static and batch <= shp.batch \
+                and max(max_qo, 1) <= shp.max_qo_len:
+            return shp
+        cap_b = batch
+        if self._qo_indptr_buf is not None:
+            cap_b = max(cap_b, self._qo_indptr_buf.numel() - 1)
+        if shp is not None and self._graph_static == static:
+            cap_b = max(cap_b, int(shp.batch))
+            max_qo = max(max_qo, int(shp.max_qo_len))
+        nq, nk, d, ps, mode, sink, window, scale = static
+        new = _lib.AttnPlan()
+        rc = lib.bsx_attn_plan_device_shape(max(cap_b, 1), nq, nk, d, ps, mode, sink, window, scale,
+                                            self._num_cus, max(max_qo, 1), ctypes.byref(new))
+        _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan")
+        self._graph_shape, self._graph_static = new, static
+        return new
+
+    @staticmethod
+    def _launch_sig(plan: _lib.AttnPlan, blob_bytes: int) -> tuple:
+        return tuple(getattr(plan, n) for n, _ in plan._fields_
+                     if n not in ("total_qo", "total_tiles")) + (blob_bytes,)
+
+    def _check_captured(self, plan: _lib.AttnPlan, blob_bytes: int) -> None:
+        """In graph mode a captured run() replays with the launch arguments it was
+        captured with; a plan that would need others is refused instead of being
+        replayed stale."""
+        if self._captured_sig is not None and self._launch_sig(plan, blob_bytes) != self._captured_sig:
+            raise ValueError(
+                "plan(): a graph captured run() of this wrapper, and this plan needs a larger "
+                "fixed shape (more requests or query tokens per request, or other heads / mask); "
+                "pass max_qo_len= to the first plan() or use a new wrapper for the new shape")
+
+    @property
+    def plan_blob(self) -> Optional[np.ndarray]:
+        """Host copy of the last host plan's schedule blob (None after a device plan)."""
+        return self._host_blob
 
     def _set_kv_indices(self, paged_kv_indices: torch.Tensor, non_blocking: bool) -> None:
         # Page ids: in graph mode run() reads the registered buffer.
@@ -271,7 +338,15 @@ class BatchPrefillWithPagedKVCacheWrapper:
             cap = max(w.numel(), 1)
             if self._use_cuda_graph and self._qo_indptr_buf is not None:
                 cap = max(cap, 32 * (self._qo_indptr_buf.numel()))
-            self._mask_words = torch.zeros(cap, dtype=torch.int32, device=self._device)
+            cmb = self._custom_mask_buf
+            if self._use_cuda_graph and cmb is not None and cmb.is_cuda \
+                    and cmb.device == self._device and cmb.is_contiguous() \
+                    and cmb.data_ptr() % 4 == 0 and cmb.numel() * cmb.element_size() >= 4 * cap:
+                # graph mode: the per-token words live in the caller's fixed mask buffer
+                # (FlashInfer packs its bit mask there), one int32 per query token
+                self._mask_words = cmb.view(torch.uint8).reshape(-1)[: 4 * cap].view(torch.int32)
+            else:
+                self._mask_words = torch.zeros(cap, dtype=torch.int32, device=self._device)
         self._mask_words[: w.numel()].copy_(w, non_blocking=True)
 
     def _plan_on_device(self, qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len,
@@ -307,20 +382,21 @@ class BatchPrefillWithPagedKVCacheWrapper:
                                             int(max_qo_len), ctypes.byref(plan))
         _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan(on_device=True)")
         blob_bytes = _align(int(plan.plan_ints) * 4)
-        if self._use_cuda_graph:
-            blob_bytes = max(self._blob_bytes, blob_bytes)
         need = blob_bytes + int(plan.float_ws_bytes)
         if need > self._ws.numel():
             raise ValueError(f"float_workspace_buffer too small: need {need} bytes, "
                              f"have {self._ws.numel()}")
+        self._check_captured(plan, blob_bytes)
         self._blob_bytes = blob_bytes
+        self._host_blob = None
         self._dev_idx = [t if t.dtype == torch.int32 and t.is_contiguous()
                          else t.to(torch.int32).contiguous()
                          for t in (qo_indptr, paged_kv_indptr, paged_kv_last_page_len)]
         blob = self._ws[: int(plan.plan_ints) * 4]
         rc = lib.bsx_attn_plan_device(ctypes.byref(plan), self._dev_idx[0].data_ptr(),
                                       self._dev_idx[1].data_ptr(), self._dev_idx[2].data_ptr(),
-                                      blob.data_ptr(), stream_of(dev))
+                                      int(paged_kv_indices.numel()), blob.data_ptr(),
+                                      stream_of(dev))
         _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan(on_device=True)")
         self._set_kv_indices(paged_kv_indices, non_blocking)
         if tree_mask_words is not None:
@@ -380,6 +456,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
                               else self._mask_words.data_ptr(),
                               out.data_ptr(), out.stride(0), _lib.ptr(lse), stream_of(dev))
         _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.run")
+        if torch.cuda.is_current_stream_capturing():
+            self._captured_sig = self._launch_sig(plan, self._blob_bytes)
         return (out, lse) if return_lse else out
 
     forward = run

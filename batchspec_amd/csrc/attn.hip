@@ -26,8 +26,9 @@
 //     over a workgroup's segments is flat: the K/V tile after the last tile of a
 //     segment is the first tile of the next segment, prefetched like any other, so a
 //     segment switch costs one Q load;
-//   * a request split over several segments writes fp32 partial results with their
-//     log-sum-exp; a second kernel merges them.  (Merging inside the main kernel,
+//   * a request split over several segments writes its partial results, normalised
+//     and rounded to the input dtype (bf16 or fp16), with their fp32 log2-sum-exp; a
+//     second kernel merges them in fp32.  (Merging inside the main kernel,
 //     by the wave that completes the last part, needs device-scope coherence for
 //     the partials across XCDs, whose L2 caches are not coherent with each other:
 //     measured on MI355X, the device-scope stores, loads and counter round trips
@@ -59,7 +60,7 @@ struct Params {
   uint16_t* out;
   int64_t out_stride;
   float* lse_out;
-  uint16_t* part_o;  // bf16 partial outputs (normalised), [slot][kv head][row][D]
+  uint16_t* part_o;  // partial outputs (normalised, input dtype), [slot][kv head][row][D]
   float* part_lse;   // their log2-sum-exp, [slot][kv head][row]
   int num_qo_heads, num_kv_heads, group;
   int page_shift, page_mask;
@@ -331,17 +332,18 @@ __device__ __forceinline__ void finish_segment(const Params& p, const Seg& cur, 
 
   if (cur.slot >= 0) {
     // Split request: publish this part for the merge kernel.  The normalised partial
-    // output is stored in bf16 (fp32's exponent range, so any input is safe; one
-    // extra rounding of 2^-9 relative), halving the partial traffic, which is
-    // written, flushed from L2 at kernel end and read back by the merge.  Plain
-    // stores: the pieces of a row combine into full lines in L2 (non-temporal
-    // stores measured 2.3x the write traffic).
+    // output is a convex combination of V rows, so the input dtype holds it; it is
+    // stored in that dtype (one extra rounding at the output's own precision, 2^-9
+    // relative for bf16 and 2^-12 for fp16), halving the partial traffic against
+    // fp32, which is written, flushed from L2 at kernel end and read back by the
+    // merge.  Plain stores: the pieces of a row combine into full lines in L2
+    // (non-temporal stores measured 2.3x the write traffic).
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       if (!rowv[nt]) continue;
       const int row = row0 + nt * 16 + c16;
       const int64_t prow = ((int64_t)cur.slot * p.num_kv_heads + h) * p.qrows_total + row;
-      store_row<BSX_DTYPE_BF16, D, NT, INTERLEAVED>(p.part_o + prow * D, g4, o, nt);
+      store_row<DT, D, NT, INTERLEAVED>(p.part_o + prow * D, g4, o, nt);
       if (g4 == 0) p.part_lse[prow] = lse2[nt];
     }
   } else {
@@ -995,8 +997,8 @@ __global__ void __launch_bounds__(256) merge_kernel(Params p) {
       wsum += w;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        acc[2 * c] += w * lo_f32<BSX_DTYPE_BF16>(v[u][c]);
-        acc[2 * c + 1] += w * hi_f32<BSX_DTYPE_BF16>(v[u][c]);
+        acc[2 * c] += w * lo_f32<DT>(v[u][c]);
+        acc[2 * c + 1] += w * hi_f32<DT>(v[u][c]);
       }
     }
     mx = m_new;

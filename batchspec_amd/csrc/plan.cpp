@@ -149,34 +149,27 @@ extern "C" int64_t bsx_attn_plan_ints_bound(int batch, int num_cus) {
          (batch + 1) + 16;
 }
 
-extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
-                             const int32_t* kv_last_page_len_h, int batch, int num_qo_heads,
-                             int num_kv_heads, int head_dim, int page_size, int mask_mode,
-                             int sink_tokens, int window_tokens, float sm_scale, int num_cus,
-                             int32_t* plan_blob_h, int64_t blob_capacity_ints,
-                             bsx_attn_plan_t* out) {
-  PLAN_REQUIRE(qo_indptr_h && kv_indptr_h && kv_last_page_len_h && plan_blob_h && out,
-               BSX_ERR_INVALID, "null argument to bsx_attn_plan");
-  PLAN_REQUIRE(batch >= 0, BSX_ERR_INVALID, "batch must be >= 0 (got %d)", batch);
-  PLAN_REQUIRE(num_kv_heads > 0 && num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0,
-               BSX_ERR_INVALID, "num_qo_heads (%d) must be a positive multiple of num_kv_heads (%d)",
-               num_qo_heads, num_kv_heads);
-  PLAN_REQUIRE(head_dim == 64 || head_dim == 128, BSX_ERR_UNSUPPORTED,
-               "head_dim %d not supported (64 or 128)", head_dim);
-  PLAN_REQUIRE(page_size >= 1 && page_size <= 1024 && (page_size & (page_size - 1)) == 0,
-               BSX_ERR_UNSUPPORTED, "page_size %d must be a power of two <= 1024", page_size);
-  PLAN_REQUIRE(mask_mode >= BSX_MASK_NONE && mask_mode <= BSX_MASK_STREAMING, BSX_ERR_INVALID,
-               "unknown mask mode %d", mask_mode);
-  PLAN_REQUIRE(num_cus >= 1, BSX_ERR_INVALID, "num_cus must be >= 1");
-  PLAN_REQUIRE(mask_mode != BSX_MASK_STREAMING || (sink_tokens >= 0 && window_tokens >= 0),
-               BSX_ERR_INVALID, "streaming view needs sink >= 0 and window >= 0");
-  PLAN_REQUIRE(qo_indptr_h[0] == 0 && kv_indptr_h[0] == 0, BSX_ERR_INVALID,
-               "qo_indptr[0] and paged_kv_indptr[0] must be 0");
-
-  const int group = num_qo_heads / num_kv_heads;
-  std::vector<int32_t> qo_len(batch), kv_len(batch);
+// Validated page table and its greedy schedule over a persistent grid of at most
+// `max_ctas` workgroups (shared by the compact and the fixed-layout host plans).
+struct HostSchedule {
+  std::vector<int32_t> qo_len, kv_len;
   int max_qo = 0;
   int safe_pos = -1;  // first position of kv_indices that belongs to a request
+  int64_t total_tiles = 0;
+  std::vector<std::vector<Seg>> per_cta;  // segments of each used workgroup
+  std::vector<int> units_of;              // segments per request
+  std::vector<int32_t> part_indptr;       // partial slots per request
+  std::vector<int32_t> merge_seqs;        // requests cut into several segments
+  int nseg = 0;
+};
+
+static int validate_table(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                          const int32_t* kv_last_page_len_h, int batch, int page_size,
+                          int mask_mode, int64_t kv_indices_len, HostSchedule* hs) {
+  PLAN_REQUIRE(qo_indptr_h[0] == 0 && kv_indptr_h[0] == 0, BSX_ERR_INVALID,
+               "qo_indptr[0] and paged_kv_indptr[0] must be 0");
+  hs->qo_len.assign(batch, 0);
+  hs->kv_len.assign(batch, 0);
   for (int b = 0; b < batch; ++b) {
     const int q = qo_indptr_h[b + 1] - qo_indptr_h[b];
     const int np = kv_indptr_h[b + 1] - kv_indptr_h[b];
@@ -187,32 +180,34 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
                  "paged_kv_last_page_len[%d] = %d outside [0, page_size=%d]", b, last, page_size);
     const int64_t kl = np > 0 ? (int64_t)(np - 1) * page_size + last : 0;
     PLAN_REQUIRE(kl < (1LL << 30), BSX_ERR_UNSUPPORTED, "kv length too large at request %d", b);
-    qo_len[b] = q;
-    kv_len[b] = (int32_t)kl;
-    if (np > 0 && safe_pos < 0) safe_pos = kv_indptr_h[b];
+    hs->qo_len[b] = q;
+    hs->kv_len[b] = (int32_t)kl;
+    if (np > 0 && hs->safe_pos < 0) hs->safe_pos = kv_indptr_h[b];
     if (mask_mode == BSX_MASK_TREE)
       PLAN_REQUIRE(q <= 32, BSX_ERR_UNSUPPORTED,
                    "tree mask supports at most 32 query tokens per request (request %d has %d)", b,
                    q);
-    max_qo = std::max(max_qo, q);
+    hs->max_qo = std::max(hs->max_qo, q);
   }
+  PLAN_REQUIRE(kv_indices_len < 0 || kv_indptr_h[batch] <= kv_indices_len, BSX_ERR_INVALID,
+               "paged_kv_indptr[-1] = %d exceeds the %lld entries of paged_kv_indices",
+               kv_indptr_h[batch], (long long)kv_indices_len);
+  return BSX_OK;
+}
 
-  const GridShape gs = grid_shape(max_qo, group, num_kv_heads, head_dim, page_size, num_cus);
-  const int qrow_tile = gs.qrow_tile, qrow_blocks = gs.qrow_blocks, hpc = gs.hpc, qbpc = gs.qbpc;
-  const int n_qgroups = gs.n_qgroups;
-  const bool shared = gs.shared;
-  const int num_ctas = gs.num_ctas;
-
+static void schedule(int batch, int mask_mode, int sink_tokens, int window_tokens, int max_ctas,
+                     HostSchedule* hs) {
   // Work units: contiguous tile ranges per request (two for the sink+window view).
   std::vector<Unit> units;
   units.reserve(2 * (size_t)batch);
-  int64_t total_tiles = 0;
+  hs->total_tiles = 0;
   for (int b = 0; b < batch; ++b) {
-    if (qo_len[b] == 0) continue;
-    const int ntiles = (kv_len[b] + kTileTokens - 1) / kTileTokens;
-    if (mask_mode == BSX_MASK_STREAMING && kv_len[b] > sink_tokens + window_tokens) {
+    if (hs->qo_len[b] == 0) continue;
+    const int kl = hs->kv_len[b];
+    const int ntiles = (kl + kTileTokens - 1) / kTileTokens;
+    if (mask_mode == BSX_MASK_STREAMING && kl > sink_tokens + window_tokens) {
       const int a_end = (sink_tokens + kTileTokens - 1) / kTileTokens;
-      const int w_beg = std::max(0, (kv_len[b] - window_tokens)) / kTileTokens;
+      const int w_beg = std::max(0, (kl - window_tokens)) / kTileTokens;
       if (w_beg <= a_end) {
         units.push_back({b, 0, ntiles});
       } else {
@@ -225,14 +220,14 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   }
   int64_t total_cost = 0;
   for (const Unit& u : units) {
-    total_tiles += u.te - u.tb;
+    hs->total_tiles += u.te - u.tb;
     total_cost += std::max(1, u.te - u.tb) + kSegmentCost;
   }
 
   // Smallest per-workgroup capacity whose greedy packing fits the grid.
-  std::vector<std::vector<Seg>> per_cta;
+  hs->per_cta.clear();
   if (!units.empty()) {
-    const int64_t W = num_ctas;
+    const int64_t W = max_ctas;
     int64_t lo = std::max<int64_t>(kSegmentCost + 1, (total_cost + W - 1) / W);
     int64_t hi = total_cost + kSegmentCost + 1;
     while (lo < hi) {
@@ -242,66 +237,112 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
       else
         lo = mid + 1;
     }
-    pack_units(units, lo, W, &per_cta);
+    pack_units(units, lo, W, &hs->per_cta);
   }
-  const int W = std::max<int>(1, (int)per_cta.size());
-  if (per_cta.empty()) per_cta.resize(1);
+  if (hs->per_cta.empty()) hs->per_cta.resize(1);
 
-  std::vector<int> units_of(batch, 0);
-  for (const auto& v : per_cta)
-    for (const Seg& sg : v) units_of[sg.b]++;
-
+  hs->units_of.assign(batch, 0);
+  hs->nseg = 0;
+  for (const auto& v : hs->per_cta) {
+    hs->nseg += (int)v.size();
+    for (const Seg& sg : v) hs->units_of[sg.b]++;
+  }
   // Partial slots for requests that ended up in more than one segment.
-  std::vector<int32_t> part_indptr(batch + 1, 0);
-  std::vector<int32_t> merge_seqs;
+  hs->part_indptr.assign(batch + 1, 0);
+  hs->merge_seqs.clear();
   for (int b = 0; b < batch; ++b) {
-    part_indptr[b + 1] = part_indptr[b] + (units_of[b] > 1 ? units_of[b] : 0);
-    if (units_of[b] > 1) merge_seqs.push_back(b);
+    const int n = hs->units_of[b];
+    hs->part_indptr[b + 1] = hs->part_indptr[b] + (n > 1 ? n : 0);
+    if (n > 1) hs->merge_seqs.push_back(b);
   }
-  const int num_partials = part_indptr[batch];
-  std::vector<int32_t> next_slot(part_indptr.begin(), part_indptr.end() - 1);
+}
 
-  int nseg = 0;
-  for (const auto& v : per_cta) nseg += (int)v.size();
-  const int64_t need =
-      4LL * batch + (W + 1) + 4LL * nseg + 3 + 4LL * (int64_t)merge_seqs.size() + (batch + 1);
-  PLAN_REQUIRE(need <= blob_capacity_ints, BSX_ERR_CAPACITY,
-               "plan blob needs %lld int32 entries, capacity %lld", (long long)need,
-               (long long)blob_capacity_ints);
-
-  int32_t* blob = plan_blob_h;
-  const int off_seq = 0;
-  const int off_seg_indptr = off_seq + 4 * batch;
-  const int off_segments = off_seg_indptr + W + 1;
-  const int off_merge = (off_segments + 4 * nseg + 3) & ~3;  // 16-byte records
-  const int off_part = off_merge + 4 * (int)merge_seqs.size();
-  for (int b = 0; b < batch; ++b) {
-    blob[off_seq + 4 * b + 0] = qo_indptr_h[b];
-    blob[off_seq + 4 * b + 1] = qo_len[b];
-    blob[off_seq + 4 * b + 2] = kv_len[b];
-    blob[off_seq + 4 * b + 3] = kv_indptr_h[b];
+// Writes seq records, seg_indptr (workgroups past the used ones get empty ranges),
+// segments, merge records and part_indptr at the given offsets.
+static void write_blob(const HostSchedule& hs, const int32_t* qo_indptr_h,
+                       const int32_t* kv_indptr_h, int batch, int blob_batch, int W,
+                       int off_seq, int off_seg_indptr, int off_segments, int off_merge,
+                       int off_part, int32_t* blob) {
+  for (int b = 0; b < blob_batch; ++b) {
+    const bool live = b < batch;
+    blob[off_seq + 4 * b + 0] = live ? qo_indptr_h[b] : qo_indptr_h[batch];
+    blob[off_seq + 4 * b + 1] = live ? hs.qo_len[b] : 0;
+    blob[off_seq + 4 * b + 2] = live ? hs.kv_len[b] : 0;
+    blob[off_seq + 4 * b + 3] = live ? kv_indptr_h[b] : kv_indptr_h[batch];
   }
+  std::vector<int32_t> next_slot(hs.part_indptr.begin(), hs.part_indptr.end() - 1);
   int si = 0;
   for (int w = 0; w < W; ++w) {
     blob[off_seg_indptr + w] = si;
-    for (const Seg& sg : per_cta[w]) {
+    if (w >= (int)hs.per_cta.size()) continue;
+    for (const Seg& sg : hs.per_cta[w]) {
       blob[off_segments + 4 * si + 0] = sg.b;
       blob[off_segments + 4 * si + 1] = sg.tb;
       blob[off_segments + 4 * si + 2] = sg.te;
-      blob[off_segments + 4 * si + 3] = units_of[sg.b] > 1 ? next_slot[sg.b]++ : -1;
+      blob[off_segments + 4 * si + 3] = hs.units_of[sg.b] > 1 ? next_slot[sg.b]++ : -1;
       ++si;
     }
   }
   blob[off_seg_indptr + W] = si;
-  for (int i = off_segments + 4 * nseg; i < off_merge; ++i) blob[i] = 0;
-  for (size_t i = 0; i < merge_seqs.size(); ++i) {
-    const int b = merge_seqs[i];
-    blob[off_merge + 4 * (int)i + 0] = part_indptr[b];
-    blob[off_merge + 4 * (int)i + 1] = part_indptr[b + 1];
+  for (int i = off_segments + 4 * si; i < off_merge; ++i) blob[i] = 0;
+  for (size_t i = 0; i < hs.merge_seqs.size(); ++i) {
+    const int b = hs.merge_seqs[i];
+    blob[off_merge + 4 * (int)i + 0] = hs.part_indptr[b];
+    blob[off_merge + 4 * (int)i + 1] = hs.part_indptr[b + 1];
     blob[off_merge + 4 * (int)i + 2] = qo_indptr_h[b];
-    blob[off_merge + 4 * (int)i + 3] = qo_len[b];
+    blob[off_merge + 4 * (int)i + 3] = hs.qo_len[b];
   }
-  for (int b = 0; b <= batch; ++b) blob[off_part + b] = part_indptr[b];
+  for (int b = 0; b <= blob_batch; ++b)
+    blob[off_part + b] = hs.part_indptr[std::min(b, batch)];
+}
+
+#define PLAN_COMMON_CHECKS()                                                                    \
+  PLAN_REQUIRE(num_kv_heads > 0 && num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0,        \
+               BSX_ERR_INVALID,                                                                 \
+               "num_qo_heads (%d) must be a positive multiple of num_kv_heads (%d)",            \
+               num_qo_heads, num_kv_heads);                                                     \
+  PLAN_REQUIRE(head_dim == 64 || head_dim == 128, BSX_ERR_UNSUPPORTED,                          \
+               "head_dim %d not supported (64 or 128)", head_dim);                              \
+  PLAN_REQUIRE(page_size >= 1 && page_size <= 1024 && (page_size & (page_size - 1)) == 0,       \
+               BSX_ERR_UNSUPPORTED, "page_size %d must be a power of two <= 1024", page_size);  \
+  PLAN_REQUIRE(mask_mode >= BSX_MASK_NONE && mask_mode <= BSX_MASK_STREAMING, BSX_ERR_INVALID,  \
+               "unknown mask mode %d", mask_mode);                                              \
+  PLAN_REQUIRE(num_cus >= 1, BSX_ERR_INVALID, "num_cus must be >= 1");                          \
+  PLAN_REQUIRE(mask_mode != BSX_MASK_STREAMING || (sink_tokens >= 0 && window_tokens >= 0),     \
+               BSX_ERR_INVALID, "streaming view needs sink >= 0 and window >= 0")
+
+extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                             const int32_t* kv_last_page_len_h, int batch, int num_qo_heads,
+                             int num_kv_heads, int head_dim, int page_size, int mask_mode,
+                             int sink_tokens, int window_tokens, float sm_scale, int num_cus,
+                             int64_t kv_indices_len, int32_t* plan_blob_h,
+                             int64_t blob_capacity_ints, bsx_attn_plan_t* out) {
+  PLAN_REQUIRE(qo_indptr_h && kv_indptr_h && kv_last_page_len_h && plan_blob_h && out,
+               BSX_ERR_INVALID, "null argument to bsx_attn_plan");
+  PLAN_REQUIRE(batch >= 0, BSX_ERR_INVALID, "batch must be >= 0 (got %d)", batch);
+  PLAN_COMMON_CHECKS();
+
+  HostSchedule hs;
+  int rc = validate_table(qo_indptr_h, kv_indptr_h, kv_last_page_len_h, batch, page_size,
+                          mask_mode, kv_indices_len, &hs);
+  if (rc != BSX_OK) return rc;
+  const int group = num_qo_heads / num_kv_heads;
+  const GridShape gs = grid_shape(hs.max_qo, group, num_kv_heads, head_dim, page_size, num_cus);
+  schedule(batch, mask_mode, sink_tokens, window_tokens, gs.num_ctas, &hs);
+  const int W = (int)hs.per_cta.size();
+  const int nseg = hs.nseg;
+  const int nmerge = (int)hs.merge_seqs.size();
+  const int64_t need = 4LL * batch + (W + 1) + 4LL * nseg + 3 + 4LL * nmerge + (batch + 1);
+  PLAN_REQUIRE(need <= blob_capacity_ints, BSX_ERR_CAPACITY,
+               "plan blob needs %lld int32 entries, capacity %lld", (long long)need,
+               (long long)blob_capacity_ints);
+  const int off_seq = 0;
+  const int off_seg_indptr = off_seq + 4 * batch;
+  const int off_segments = off_seg_indptr + W + 1;
+  const int off_merge = (off_segments + 4 * nseg + 3) & ~3;  // 16-byte records
+  const int off_part = off_merge + 4 * nmerge;
+  write_blob(hs, qo_indptr_h, kv_indptr_h, batch, batch, W, off_seq, off_seg_indptr,
+             off_segments, off_merge, off_part, plan_blob_h);
 
   memset(out, 0, sizeof(*out));
   out->batch = batch;
@@ -311,16 +352,16 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   out->page_size = page_size;
   out->mask_mode = mask_mode;
   out->group_size = group;
-  out->qrow_tile = qrow_tile;
-  out->qrow_blocks = qrow_blocks;
-  out->heads_per_cta = hpc;
-  out->qblocks_per_cta = qbpc;
-  out->num_qgroups = n_qgroups;
+  out->qrow_tile = gs.qrow_tile;
+  out->qrow_blocks = gs.qrow_blocks;
+  out->heads_per_cta = gs.hpc;
+  out->qblocks_per_cta = gs.qbpc;
+  out->num_qgroups = gs.n_qgroups;
   out->num_ctas = W;
   out->num_segments = nseg;
-  out->num_partials = num_partials;
-  out->num_split_requests = (int)merge_seqs.size();
-  out->max_qo_len = max_qo;
+  out->num_partials = hs.part_indptr[batch];
+  out->num_split_requests = nmerge;
+  out->max_qo_len = hs.max_qo;
   out->tile_tokens = kTileTokens;
   out->sink_tokens = sink_tokens;
   out->window_tokens = window_tokens;
@@ -330,14 +371,58 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   out->off_merge_seqs = off_merge;
   out->off_part_indptr = off_part;
   out->plan_ints = (int32_t)need;
-  const int64_t rows_total = (int64_t)qrow_tile * qrow_blocks;
-  // partial outputs in bf16 plus their fp32 log-sum-exp
-  out->float_ws_bytes = (int64_t)num_partials * num_kv_heads * rows_total * (head_dim * 2 + 4);
+  const int64_t rows_total = (int64_t)gs.qrow_tile * gs.qrow_blocks;
+  // partial outputs in the input dtype plus their fp32 log-sum-exp
+  out->float_ws_bytes =
+      (int64_t)out->num_partials * num_kv_heads * rows_total * (head_dim * 2 + 4);
   out->sm_scale = sm_scale > 0.f ? sm_scale : 1.0f / std::sqrt((float)head_dim);
   out->total_qo = batch > 0 ? qo_indptr_h[batch] : 0;
-  out->safe_page_pos = safe_pos;
-  out->total_tiles = total_tiles;
-  out->shared_kv_tiles = shared ? 1 : 0;
+  out->safe_page_pos = hs.safe_pos;
+  out->total_tiles = hs.total_tiles;
+  out->shared_kv_tiles = gs.shared ? 1 : 0;
+  out->off_dyn = -1;
+  return BSX_OK;
+}
+
+extern "C" int bsx_attn_plan_fixed(const bsx_attn_plan_t* shape, const int32_t* qo_indptr_h,
+                                   const int32_t* kv_indptr_h,
+                                   const int32_t* kv_last_page_len_h, int batch,
+                                   int64_t kv_indices_len, int32_t* plan_blob_h,
+                                   int64_t blob_capacity_ints, bsx_attn_plan_t* out) {
+  PLAN_REQUIRE(shape && qo_indptr_h && kv_indptr_h && kv_last_page_len_h && plan_blob_h && out,
+               BSX_ERR_INVALID, "null argument to bsx_attn_plan_fixed");
+  PLAN_REQUIRE(shape->device_plan == 1, BSX_ERR_INVALID,
+               "shape was not made by bsx_attn_plan_device_shape");
+  PLAN_REQUIRE(batch >= 1 && batch <= shape->batch, BSX_ERR_INVALID,
+               "batch %d outside the fixed shape's 1..%d requests", batch, shape->batch);
+  PLAN_REQUIRE(blob_capacity_ints >= shape->plan_ints, BSX_ERR_CAPACITY,
+               "plan blob needs %d int32 entries, capacity %lld", shape->plan_ints,
+               (long long)blob_capacity_ints);
+  HostSchedule hs;
+  int rc = validate_table(qo_indptr_h, kv_indptr_h, kv_last_page_len_h, batch,
+                          shape->page_size, shape->mask_mode, kv_indices_len, &hs);
+  if (rc != BSX_OK) return rc;
+  PLAN_REQUIRE(hs.max_qo <= shape->max_qo_len, BSX_ERR_CAPACITY,
+               "a request has %d query tokens, the fixed shape allows %d", hs.max_qo,
+               shape->max_qo_len);
+  PLAN_REQUIRE(hs.safe_pos >= 0, BSX_ERR_INVALID, "the page table holds no page");
+  schedule(batch, shape->mask_mode, shape->sink_tokens, shape->window_tokens, shape->num_ctas,
+           &hs);
+  const int W = shape->num_ctas;
+  PLAN_REQUIRE(hs.nseg <= shape->num_segments, BSX_ERR_CAPACITY,
+               "schedule of %d segments exceeds the fixed bound %d", hs.nseg,
+               shape->num_segments);
+  write_blob(hs, qo_indptr_h, kv_indptr_h, batch, shape->batch, W, shape->off_seq,
+             shape->off_seg_indptr, shape->off_segments, shape->off_merge_seqs,
+             shape->off_part_indptr, plan_blob_h);
+  int32_t* dyn = plan_blob_h + shape->off_dyn;
+  dyn[0] = (int32_t)hs.merge_seqs.size();
+  dyn[1] = 0;
+  dyn[2] = hs.nseg;
+  dyn[3] = 0;
+  *out = *shape;
+  out->total_qo = qo_indptr_h[batch];
+  out->total_tiles = hs.total_tiles;
   return BSX_OK;
 }
 

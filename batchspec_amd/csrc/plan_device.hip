@@ -19,7 +19,8 @@
 //                     (which is workgroup order), with partial slots for requests cut
 //                     into several segments and one merge record per such request;
 //   dyn             = {split requests, error code, segments, 0}.
-// A malformed table leaves an empty schedule and the most negative error code of its
+// A malformed table (including one whose kv_indptr[B] exceeds the entries of
+// kv_indices) leaves an empty schedule and the most negative error code of its
 // violations (no output is written); the launch itself never fails on data.
 #include "common.h"
 #include "attn_shape.h"
@@ -40,6 +41,7 @@ struct Args {
   const int32_t* kv_indptr;
   const int32_t* last_len;
   int32_t* blob;
+  int64_t kv_indices_len;  // entries of kv_indices (< 0: not checked)
   int B, W, page_size, mask_mode, sink, window, max_qo;
   int off_seg_indptr, off_segments, off_merge, off_part, off_dyn;
 };
@@ -146,7 +148,9 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(Args a) {
     if (b < B) s_cpre[b] = carry + pre;
     carry += tot;
   }
-  if (t == 0 && a.kv_indptr[B] < 1) atomicMin(&s_err, (int)BSX_ERR_INVALID);
+  if (t == 0 && (a.kv_indptr[B] < 1 ||
+                 (a.kv_indices_len >= 0 && a.kv_indptr[B] > a.kv_indices_len)))
+    atomicMin(&s_err, (int)BSX_ERR_INVALID);
   __syncthreads();
   const int err = s_err;
   const int64_t T = err ? 0 : carry;
@@ -241,7 +245,7 @@ using namespace bsx;
 
 extern "C" int bsx_attn_plan_device(const bsx_attn_plan_t* plan, const int32_t* qo_indptr_d,
                                     const int32_t* kv_indptr_d, const int32_t* kv_last_page_len_d,
-                                    int32_t* plan_blob_d, void* stream) {
+                                    int64_t kv_indices_len, int32_t* plan_blob_d, void* stream) {
   BSX_REQUIRE(plan != nullptr && plan->device_plan == 1, BSX_ERR_INVALID,
               "plan was not made by bsx_attn_plan_device_shape");
   BSX_REQUIRE(plan->batch >= 1 && plan->batch <= attn_shape::kMaxDevicePlanBatch,
@@ -253,6 +257,7 @@ extern "C" int bsx_attn_plan_device(const bsx_attn_plan_t* plan, const int32_t* 
   a.kv_indptr = kv_indptr_d;
   a.last_len = kv_last_page_len_d;
   a.blob = plan_blob_d;
+  a.kv_indices_len = kv_indices_len;
   a.B = plan->batch;
   a.W = plan->num_ctas;
   a.page_size = plan->page_size;

@@ -118,13 +118,28 @@ int64_t bsx_attn_plan_ints_bound(int batch, int num_cus);
  * a persistent grid sized to fill `num_cus` compute units.  Host-only; no GPU
  * needed.
  *   qo_indptr_h[batch+1], kv_indptr_h[batch+1], kv_last_page_len_h[batch]
+ *   kv_indices_len: entries of the paged_kv_indices tensor run() will read;
+ *   kv_indptr_h[batch] beyond it is rejected (negative: not checked).
  *   sm_scale <= 0 means 1/sqrt(head_dim). */
 int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
                   const int32_t* kv_last_page_len_h, int batch, int num_qo_heads,
                   int num_kv_heads, int head_dim, int page_size, int mask_mode,
                   int sink_tokens, int window_tokens, float sm_scale, int num_cus,
-                  int32_t* plan_blob_h, int64_t blob_capacity_ints,
+                  int64_t kv_indices_len, int32_t* plan_blob_h, int64_t blob_capacity_ints,
                   bsx_attn_plan_t* plan_out);
+
+/* The same host schedule written into the fixed, bound-sized blob layout of a shape
+ * made by bsx_attn_plan_device_shape (below) for the wrapper's use_cuda_graph=True
+ * mode (batchspec/backends/base/attn_wrapper.py:53-57): every launch argument of
+ * bsx_attn_run (grid, blob offsets, workspace layout, merge grid) depends on the
+ * shape only, so a graph that captured run() stays valid when plan() is called again
+ * with other lengths, as FlashInfer's graph mode allows.  batch <= shape->batch
+ * (requests past `batch` are empty); every query length <= shape->max_qo_len; the
+ * table must hold a page.  plan_out = *shape with total_qo and total_tiles set. */
+int bsx_attn_plan_fixed(const bsx_attn_plan_t* shape, const int32_t* qo_indptr_h,
+                        const int32_t* kv_indptr_h, const int32_t* kv_last_page_len_h,
+                        int batch, int64_t kv_indices_len, int32_t* plan_blob_h,
+                        int64_t blob_capacity_ints, bsx_attn_plan_t* plan_out);
 
 /* Device-side planning (no counterpart in the reference, whose plan() always
  * schedules on the host from host copies of the page table,
@@ -142,7 +157,8 @@ int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
  * cost shares of the fixed grid (a tile costs 1, a segment start 2, as in
  * bsx_attn_plan).  Requirements checked on the device: indptrs non-decreasing from
  * 0, last-page lengths in [0, page_size], query lengths at most max_qo_len (32 in
- * tree mode), and at least one page in the table; a violation writes an error code
+ * tree mode), at least one page in the table and kv_indptr[batch] <= kv_indices_len
+ * (when kv_indices_len >= 0); a violation writes an error code
  * (BSX_ERR_*) into blob[off_dyn + 1] and an empty schedule (no output is written),
  * otherwise 0.  A device plan's total_qo is the bound batch * max_qo_len: q and out
  * passed to bsx_attn_run need that many token rows. */
@@ -152,7 +168,7 @@ int bsx_attn_plan_device_shape(int batch, int num_qo_heads, int num_kv_heads, in
                                bsx_attn_plan_t* plan_out);
 int bsx_attn_plan_device(const bsx_attn_plan_t* plan, const int32_t* qo_indptr_d,
                          const int32_t* kv_indptr_d, const int32_t* kv_last_page_len_d,
-                         int32_t* plan_blob_d, void* stream);
+                         int64_t kv_indices_len, int32_t* plan_blob_d, void* stream);
 
 /* Replaces BatchPrefillWithPagedKVCacheWrapper.run(q, paged_kv_cache) as called
  * at batchspec/models/modules/attention/standard.py:69.

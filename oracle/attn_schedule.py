@@ -57,7 +57,7 @@ def layout(B: int, W: int):
 
 
 def schedule(qo_indptr, kv_indptr, last, page_size: int, mask_mode: int, sink: int, window: int,
-             max_qo: int, W: int):
+             max_qo: int, W: int, kv_indices_len: int = -1):
     """Expected blob entries: dict of the written parts (unwritten slots are not compared)."""
     qo = np.asarray(qo_indptr, np.int64)
     kvp = np.asarray(kv_indptr, np.int64)
@@ -80,7 +80,7 @@ def schedule(qo_indptr, kv_indptr, last, page_size: int, mask_mode: int, sink: i
             e = ERR_UNSUPPORTED
         err = min(err, e)  # the most negative code of all violations
         seq.append((int(q0), 0 if e else int(qlen), 0 if e else int(kl), int(p0)))
-    if kvp[B] < 1:
+    if kvp[B] < 1 or (kv_indices_len >= 0 and kvp[B] > kv_indices_len):
         err = min(err, ERR_INVALID)
     units = [units_of(s[1], s[2], mask_mode, sink, window) for s in seq]
     cpre, c = [], 0

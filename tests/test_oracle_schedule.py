@@ -75,7 +75,7 @@ def test_device_shape_layout(B, hq, hkv, d, max_qo, mode):
     blob = np.empty(bound, np.int32)
     hp = _lib.AttnPlan()
     rc = lib.bsx_attn_plan(qo.ctypes.data, kvp.ctypes.data, last.ctypes.data, B, hq, hkv, d, 16,
-                           mode, 64 if mode == 3 else 0, 512 if mode == 3 else 0, 0.0, 256,
+                           mode, 64 if mode == 3 else 0, 512 if mode == 3 else 0, 0.0, 256, -1,
                            blob.ctypes.data, bound, ctypes.byref(hp))
     assert rc == 0
     for f in ("qrow_tile", "qrow_blocks", "heads_per_cta", "qblocks_per_cta", "num_qgroups",
@@ -102,9 +102,89 @@ def test_device_plan_entry_rejects_bad_arguments():
     buf = np.zeros(16, np.int32)
     p = buf.ctypes.data
     # a host plan (device_plan == 0) is refused
-    assert lib.bsx_attn_plan_device(ctypes.byref(plan), p, p, p, p, None) == -1
+    assert lib.bsx_attn_plan_device(ctypes.byref(plan), p, p, p, -1, p, None) == -1
     rc = lib.bsx_attn_plan_device_shape(4, 32, 8, 128, 16, 1, 0, 0, 0.0, 256, 5, ctypes.byref(plan))
     assert rc == 0
     # null device pointers are refused
-    assert lib.bsx_attn_plan_device(ctypes.byref(plan), None, p, p, p, None) == -1
-    assert lib.bsx_attn_plan_device(ctypes.byref(plan), p, p, p, None, None) == -1
+    assert lib.bsx_attn_plan_device(ctypes.byref(plan), None, p, p, -1, p, None) == -1
+    assert lib.bsx_attn_plan_device(ctypes.byref(plan), p, p, p, -1, None, None) == -1
+
+
+def _fixed_plan(lib, shape, qo, kvp, last, nidx=-1):
+    qo, kvp, last = (np.ascontiguousarray(a, dtype=np.int32) for a in (qo, kvp, last))
+    blob = np.full(int(shape.plan_ints), -7, np.int32)
+    plan = _lib.AttnPlan()
+    rc = lib.bsx_attn_plan_fixed(ctypes.byref(shape), qo.ctypes.data, kvp.ctypes.data,
+                                 last.ctypes.data, len(qo) - 1, nidx, blob.ctypes.data,
+                                 int(shape.plan_ints), ctypes.byref(plan))
+    return rc, plan, blob
+
+
+@pytest.mark.parametrize("mode,max_qo", [(1, 5), (2, 32), (3, 1)])
+def test_fixed_layout_host_plan_keeps_every_launch_argument(mode, max_qo):
+    """Graph mode: host plans of changing lengths (and fewer requests) laid out in one
+    bound-sized shape keep every launch argument of bsx_attn_run, and each blob is a
+    valid schedule (every tile once, slots and merge records consistent)."""
+    lib = _lib.load()
+    sink, window = (64, 512) if mode == 3 else (0, 0)
+    shape = _lib.AttnPlan()
+    assert lib.bsx_attn_plan_device_shape(64, 32, 8, 128, 16, mode, sink, window, 0.0, 256,
+                                          max_qo, ctypes.byref(shape)) == 0
+    skip = ("total_qo", "total_tiles")
+    rng = np.random.default_rng(mode)
+    for it in range(12):
+        B = int(rng.integers(1, 65))
+        qo_l = rng.integers(0 if it % 3 == 0 else 1, max_qo + 1, B)
+        ctx = rng.integers(0, 9000 if mode != 3 else 70000, B)
+        kv = ctx + qo_l
+        pages = np.maximum(1, (kv + 15) // 16)
+        last = np.where(kv > 0, (kv - 1) % 16 + 1, 0)
+        kvp = np.concatenate([[0], np.cumsum(pages)])
+        qo = np.concatenate([[0], np.cumsum(qo_l)])
+        rc, plan, blob = _fixed_plan(lib, shape, qo, kvp, last, int(kvp[-1]))
+        assert rc == 0, lib.bsx_last_error()
+        for name, _ in shape._fields_:
+            if name not in skip:
+                assert getattr(plan, name) == getattr(shape, name), name
+        assert plan.total_qo == qo[-1]
+        s = OS.read_blob(blob, shape.batch, shape.num_ctas)
+        assert s["dyn"][1] == 0
+        OS.check_invariants(s, qo, kvp, last, 16, mode, sink, window)
+        # requests past B are empty records that no segment names
+        assert (s["seq"][B:, 1] == 0).all() and (s["seq"][B:, 2] == 0).all()
+        assert (s["segments"][:, 0] < B).all()
+        assert int(s["dyn"][2]) <= shape.num_segments
+
+
+def test_fixed_layout_host_plan_rejects():
+    lib = _lib.load()
+    shape = _lib.AttnPlan()
+    assert lib.bsx_attn_plan_device_shape(4, 32, 8, 128, 16, 1, 0, 0, 0.0, 256, 5,
+                                          ctypes.byref(shape)) == 0
+    qo, kvp, last = [0, 5, 10], [0, 3, 9], [16, 4]
+    assert _fixed_plan(lib, shape, qo, kvp, last, 9)[0] == 0
+    # more query tokens than the fixed shape allows
+    assert _fixed_plan(lib, shape, [0, 6, 11], kvp, last, 9)[0] == _lib.BSX_ERR_CAPACITY
+    # the page table points past the kv_indices tensor
+    assert _fixed_plan(lib, shape, qo, kvp, last, 8)[0] == _lib.BSX_ERR_INVALID
+    # more requests than the shape
+    assert _fixed_plan(lib, shape, [0, 1, 2, 3, 4, 5], [0, 1, 2, 3, 4, 5], [1] * 5)[0] != 0
+    # a table without any page (run() has nothing to read)
+    assert _fixed_plan(lib, shape, [0, 1, 2], [0, 0, 0], [0, 0])[0] == _lib.BSX_ERR_INVALID
+    # a compact host plan refuses the same overflowing table
+    bound = int(lib.bsx_attn_plan_ints_bound(2, 256))
+    blob = np.empty(bound, np.int32)
+    a = [np.ascontiguousarray(x, dtype=np.int32) for x in (qo, kvp, last)]
+    rc = lib.bsx_attn_plan(a[0].ctypes.data, a[1].ctypes.data, a[2].ctypes.data, 2, 32, 8, 128, 16,
+                           1, 0, 0, 0.0, 256, 8, blob.ctypes.data, bound,
+                           ctypes.byref(_lib.AttnPlan()))
+    assert rc == _lib.BSX_ERR_INVALID and b"exceeds" in lib.bsx_last_error()
+
+
+def test_device_schedule_oracle_flags_an_overflowing_table():
+    """The restatement of the device planner rejects kv_indptr[B] beyond the entries of
+    kv_indices with an empty schedule, as the kernel does."""
+    s = OS.schedule([0, 5, 10], [0, 3, 9], [16, 4], 16, 1, 0, 0, 5, 8, kv_indices_len=8)
+    assert s["dyn"][1] == OS.ERR_INVALID and len(s["segments"]) == 0
+    s = OS.schedule([0, 5, 10], [0, 3, 9], [16, 4], 16, 1, 0, 0, 5, 8, kv_indices_len=9)
+    assert s["dyn"][1] == 0 and len(s["segments"]) > 0
