@@ -213,3 +213,37 @@ def test_evaluate_posterior_sampling_branch():
     np.testing.assert_array_equal(acc.cpu().numpy(), emi + 1)
     np.testing.assert_array_equal(bonus[:, 0].cpu().numpy(), out[np.arange(16), emi])
     np.testing.assert_array_equal(eos[:, 0].cpu().numpy(), (out == 7).any(1))
+
+
+def test_greedy_graph_keeps_its_workspace_after_a_larger_call():
+    """A graph captured at a small batch replays into the workspace it captured, even
+    after an eager call at a larger batch has grown the cached workspace: the outgrown
+    buffer is kept, so no tensor allocated afterwards shares its memory."""
+    say("greedy: capture at B=16, eager at B=64, then replay")
+    from batchspec_amd import posterior
+    posterior._WS.clear()
+    small = greedy_case(B=16, k=4, V=128256, seed=16, dtype=torch.bfloat16)
+    big = greedy_case(B=64, k=4, V=128256, seed=64, dtype=torch.bfloat16)
+    ds, ls = small.draft_tokens.to(DEV), small.target_logits.to(DEV)
+    ref = OAc.greedy_posterior(small.draft_tokens.numpy(), small.target_logits.float().numpy(),
+                               -1, "reference")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        bsx.evaluate_posterior(ds, ls, greedy=True, eos_token_id=-1)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = bsx.evaluate_posterior(ds, ls, greedy=True, eos_token_id=-1)
+    bsx.evaluate_posterior(big.draft_tokens.to(DEV), big.target_logits.to(DEV), greedy=True,
+                           eos_token_id=-1)
+    nbytes = posterior._WS["__retired__"][-1].numel()
+    probes = [torch.full((nbytes // 4,), 12345, dtype=torch.int32, device=DEV) for _ in range(4)]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(outs[0].cpu().numpy(), ref[0], err_msg=f"replay {rep}")
+        np.testing.assert_array_equal(outs[1].cpu().numpy(), ref[1], err_msg=f"replay {rep}")
+        for p in probes:
+            assert bool((p == 12345).all()), f"replay {rep} wrote into a live tensor"
