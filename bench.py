@@ -14,20 +14,23 @@ Printed: one JSON line with
               on the stream the kernels run on (the pass is the attention kernel
               plus, for split requests, the merge of their partial results)
   roofline    the same pass against the 8 TB/s HBM peak; `traffic` is the HBM
-              bytes per pass measured with rocprofv3 counters (profiles/)
-  accepted_tok_s  accepted tokens/s of a 32-layer verify step: 32 x (append +
-              attention) + fused greedy acceptance over [64, 5, 128256] bf16 logits
-              (draft = target argmax with probability 0.7), reference acceptance rule
-  stochastic_accept  config 5 (B=128, k=5, V=128256, bf16): time and HBM fraction
-  cpu_baseline    the fp32 CPU oracle on a bounded sample of the same workload
+              bytes per pass and `mfma_util` the matrix-core use of the attention
+              kernel, both from the committed rocprofv3 counter summaries (profiles/)
+  greedy_accept / stochastic_accept   acceptance at [64, 5, 128256] (config-2 shape)
+              and config 5 (B=128, k=5, V=128256), time and HBM fraction
+  config4_tree_attention / config3b_verify_attention / config3a_draft_attention
+              verify attention at the other BASELINE configurations
+  accepted_tok_s  accepted tokens/s of a 32-layer verify step: the page-table update
+              (insert + delete), one device plan, 32 x (append + attention) and the
+              fused greedy acceptance over [64, 5, 128256] bf16 logits (draft = target
+              argmax with probability 0.7), reference acceptance rule
+  cpu_baseline    torch fp32 paged gather + scaled_dot_product_attention over the
+              config-2 batch on the host cores (median of 5 runs after 1 warmup), and
+              the C acceptance restatement over config 5
 
-`--extra-configs` adds verify attention at configs 4 (EAGLE trees), 3b (long context)
-and 3a (sink+window draft view), the device tree masks of config 4, one step of the
-sync-free page-table update at B=64 beside the host-synchronising torch mirror, and the
-device-side attention schedule at config 2 with the attention pass run on it.
-
-`--calibrate-copy` instead times a plain 1 GiB device copy (the known-size kernel
-the HBM byte counters are scaled against).
+`--only NAME` (attn2, accept, attn4, attn3b, attn3a) times one part alone, for the
+counter runs of rocprofv3; `--calibrate-copy` times a plain 1 GiB device copy (the
+known-size kernel the HBM byte counters are scaled against).
 """
 from __future__ import annotations
 
@@ -44,7 +47,10 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "verify-attn HBM GB/s (% of 8 TB/s) + accepted tok/s, Llama-8B shape B=64 k=4"
-TRAFFIC_FILE = ROOT / "profiles" / "verify_attn_config2_traffic.txt"
+PROFILES = ROOT / "profiles"
+TRAFFIC_FILE = PROFILES / "verify_attn_config2_traffic.txt"
+MFMA_FILE = PROFILES / "verify_attn_mfma_counters.txt"
+NUM_LAYERS = 32
 
 
 def attn_bytes(b) -> int:
@@ -86,63 +92,86 @@ def time_events(fn, iters: int, warmup: int):
     return [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
 
 
+def mean(xs):
+    return sum(xs) / len(xs)
+
+
 def median(xs):
     s = sorted(xs)
-    return s[len(s) // 2]
+    n = len(s)
+    return s[n // 2] if n % 2 else 0.5 * (s[n // 2 - 1] + s[n // 2])
 
 
-def measured_traffic():
-    """HBM bytes per attention pass from the committed rocprofv3 counter summary."""
-    if not TRAFFIC_FILE.exists():
+def log(msg: str) -> None:
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
+def profile_value(path: Path, key: str):
+    """A `key: value` line of a committed rocprofv3 summary (None when absent)."""
+    if not path.exists():
         return None
-    m = re.search(r"^traffic_bytes_per_pass:\s*(\d+)", TRAFFIC_FILE.read_text(), re.M)
-    return int(m.group(1)) if m else None
+    m = re.search(rf"^{re.escape(key)}:\s*([-+0-9.eE]+)", path.read_text(), re.M)
+    if not m:
+        return None
+    v = float(m.group(1))
+    return int(v) if v.is_integer() else v
 
 
-def extra_configs(dev, iters: int):
-    """Verify attention at configs 4 (EAGLE tree), 3b (long context, split-KV) and 3a
-    (the MagicDec draft over a 64-sink + 512-window view), each over rotating input sets
-    (one for 3b: 6.4 GB of KV), timed like the headline pass."""
-    import numpy as np
+def attention_pass(dev, sets, plan_kw, iters, warmup=3, ws_mb=512):
+    """Plan one wrapper per input set and time run() over the rotating sets."""
     import torch
     import batchspec_amd as bsx
-    from batchspec_amd.workloads import config3, config4, make_verify_batch
+    wr, outs = [], []
+    for b in sets:
+        w = bsx.BatchPrefillWithPagedKVCacheWrapper(
+            torch.empty(ws_mb << 20, dtype=torch.uint8, device=dev), "NHD")
+        kw = dict(plan_kw)
+        if kw.pop("tree", False):
+            kw["tree_mask_words"] = b.mask_words
+        w.plan(b.qo_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, b.num_qo_heads,
+               b.num_kv_heads, b.head_dim, b.page_size, q_data_type=torch.bfloat16, **kw)
+        wr.append(w)
+        outs.append(torch.empty_like(b.q))
+    k = len(sets)
+    us = time_events(lambda i: wr[i % k].run(sets[i % k].q, sets[i % k].cache, out=outs[i % k]),
+                     iters, warmup)
+    return wr, us
 
-    def run(name, sets, plan_kw, nbytes, n):
-        ws = [torch.empty(512 << 20, dtype=torch.uint8, device=dev) for _ in sets]
-        wr = []
-        for b, w_buf in zip(sets, ws):
-            w = bsx.BatchPrefillWithPagedKVCacheWrapper(w_buf, "NHD")
-            kw = dict(plan_kw)
-            if kw.pop("tree", False):
-                kw["tree_mask_words"] = b.mask_words
-            w.plan(b.qo_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, b.num_qo_heads,
-                   b.num_kv_heads, b.head_dim, b.page_size, q_data_type=torch.bfloat16, **kw)
-            wr.append(w)
-        outs = [torch.empty_like(b.q) for b in sets]
-        k = len(sets)
-        us = time_events(lambda i: wr[i % k].run(sets[i % k].q, sets[i % k].cache, out=outs[i % k]),
-                         n, 3)
-        t = sum(us) / len(us)
-        nb = sum(nbytes) / k
-        p = wr[0].plan_info
-        return {"us": round(t, 2), "GB/s": round(nb / t / 1e3, 1),
-                "frac": round(nb / t / 1e3 / HBM_PEAK_GBS, 4), "bytes": int(nb),
-                "plan": {"workgroups": int(p.num_ctas), "segments": int(p.num_segments),
-                         "split_requests": int(p.num_split_requests),
-                         "shared_kv_tiles": int(p.shared_kv_tiles),
-                         "heads_per_workgroup": int(p.heads_per_cta),
-                         "waves_per_head": int(p.qblocks_per_cta)}}
 
-    out = {}
+def pass_record(wr, us, nbytes):
+    t = mean(us)
+    p = wr[0].plan_info
+    return {"us": round(t, 2), "us_median": round(median(us), 2), "GB/s": round(nbytes / t / 1e3, 1),
+            "frac": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "bytes": int(nbytes),
+            "plan": {"workgroups": int(p.num_ctas), "segments": int(p.num_segments),
+                     "split_requests": int(p.num_split_requests),
+                     "shared_kv_tiles": int(p.shared_kv_tiles),
+                     "heads_per_workgroup": int(p.heads_per_cta),
+                     "waves_per_head": int(p.qblocks_per_cta)}}
+
+
+def config4_attention(dev, iters):
+    from batchspec_amd.workloads import config4
     s4 = [config4(device=dev, seed=1004 + i) for i in range(3)]
-    out["config4_tree_attention"] = run("4", s4, dict(causal=False, tree=True),
-                                        [attn_bytes(b) for b in s4], iters)
-    del s4
+    wr, us = attention_pass(dev, s4, dict(causal=False, tree=True), iters)
+    rec = pass_record(wr, us, mean([attn_bytes(b) for b in s4]))
+    rec["workload"] = "B=32, ctx U[2048,8192], 32-node draft trees (ancestor bitmask), 32/8 heads"
+    return rec
+
+
+def config3b_attention(dev, iters):
+    from batchspec_amd.workloads import config3
     s3 = [config3(device=dev, seed=1003)]
-    out["config3b_verify_attention"] = run("3b", s3, dict(causal=True), [attn_bytes(s3[0])],
-                                           max(5, iters // 3))
-    del s3
+    wr, us = attention_pass(dev, s3, dict(causal=True), max(5, iters // 3))
+    rec = pass_record(wr, us, attn_bytes(s3[0]))
+    rec["workload"] = "B=32, ctx U[32768,65536], 5 causal queries, split-KV + merge"
+    return rec
+
+
+def config3a_attention(dev, iters):
+    import numpy as np
+    import torch
+    from batchspec_amd.workloads import make_verify_batch
     s3a = [make_verify_batch(32, 32768, 65536, 1, 32, 8, 128, 16, dtype=torch.bfloat16,
                              scale=0.5, seed=1003 + i, device=dev) for i in range(2)]
 
@@ -150,24 +179,71 @@ def extra_configs(dev, iters: int):
         view = int(np.sum(np.minimum(b.kv_lens, 576)))
         return (view * b.num_kv_heads * b.head_dim * 4 + 2 * b.q.numel() * 2
                 + int(np.sum(np.minimum(np.diff(b.kv_indptr.cpu().numpy()), 36 + 1))) * 4)
-    out["config3a_draft_attention"] = run("3a", s3a, dict(causal=True, sink_tokens=64,
-                                                          window_tokens=512),
-                                          [view_bytes(b) for b in s3a], iters)
-    del s3a
+    wr, us = attention_pass(dev, s3a, dict(causal=True, sink_tokens=64, window_tokens=512), iters)
+    rec = pass_record(wr, us, mean([view_bytes(b) for b in s3a]))
+    rec["workload"] = "B=32, ctx U[32768,65536], 1 query over a 64-sink + 512-window view"
+    return rec
 
-    # Verify-step plumbing: the config-4 tree masks built on the device, and one step's
-    # page-table update (insert the 25 MTP tokens, delete the rejected ones) at the
-    # config-2 batch, against the host-synchronising torch mirror of the reference.
-    import time
+
+def acceptance(dev, iters, out):
+    """Greedy acceptance at the config-2 shape and stochastic acceptance at config 5."""
+    import torch
+    import batchspec_amd as bsx
+    from batchspec_amd.workloads import greedy_case, stochastic_case
+    g = greedy_case(B=64, k=4, V=128256, p_match=0.7, seed=2002, dtype=torch.bfloat16)
+    gl, gd = g.target_logits.to(dev), g.draft_tokens.to(dev)
+    acc_us = time_events(lambda i: bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1),
+                         iters, 3)
+    _, acc_ref, _ = bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1)
+    _, acc_pre, _ = bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1,
+                                           accept_rule="prefix")
+    t_acc = mean(acc_us)
+    gbytes = gl.numel() * 2
+    out["greedy_accept"] = {"us": round(t_acc, 2), "GB/s": round(gbytes / t_acc / 1e3, 1),
+                            "frac": round(gbytes / t_acc / 1e3 / HBM_PEAK_GBS, 4),
+                            "bytes": gbytes, "workload": "[64, 5, 128256] bf16 logits, fused argmax"}
+    del gl, g
+    s = stochastic_case(device=dev)
+    n = max(5, iters // 3)
+    st_us = time_events(lambda i: bsx.sampling.chain_speculative_sampling_from_logits(
+        s.draft_logits, s.draft_tokens, s.target_logits, 1.0, uniforms=s.uniforms), n, 2)
+    t_st = mean(st_us)
+    sbytes = (s.target_logits.numel() + s.draft_logits.numel()) * 2
+    out["stochastic_accept"] = {"us": round(t_st, 2), "GB/s": round(sbytes / t_st / 1e3, 1),
+                                "frac": round(sbytes / t_st / 1e3 / HBM_PEAK_GBS, 4),
+                                "bytes": sbytes,
+                                "workload": "config 5: B=128, k=5, V=128256 bf16, T=1, draft logits"}
+    # the same acceptance with the reference's default filters (top_k=20, top_p=0.95)
+    # applied to both distributions
+    sf_us = time_events(lambda i: bsx.sampling.chain_speculative_sampling_from_logits(
+        s.draft_logits, s.draft_tokens, s.target_logits, 1.0, uniforms=s.uniforms,
+        top_k=20, top_p=0.95), n, 2)
+    t_sf = mean(sf_us)
+    out["stochastic_accept_top_k20_top_p095"] = {
+        "us": round(t_sf, 2), "GB/s": round(sbytes / t_sf / 1e3, 1),
+        "frac": round(sbytes / t_sf / 1e3 / HBM_PEAK_GBS, 4), "bytes": sbytes}
+    return t_acc, acc_ref, acc_pre
+
+
+def step_plumbing(dev, iters, sets, acc_ref):
+    """Per-step work around the 32 layers: the sync-free page-table update (insert the
+    25 MTP tokens of a step, delete the rejected ones) at B=64, the device plan at
+    config 2 with the attention pass run on it, the host plan's wall time, the config-4
+    tree masks and the accepted-KV compaction."""
+    import numpy as np
+    import torch
+    import batchspec_amd as bsx
+    from batchspec_amd.collate import collate_accepted_kv_cache
     from batchspec_amd.masks import tree_masks
-    from batchspec_amd.page_table import DevicePageTable, PageTable
+    from batchspec_amd.page_table import DevicePageTable
     from batchspec_amd.workloads import random_tree_parents
+    out = {}
     rng = np.random.default_rng(1004)
     par = torch.from_numpy(np.stack([random_tree_parents(32, rng) for _ in range(32)])
                            .astype(np.int32)).to(dev)
     cl = torch.from_numpy(rng.integers(2048, 8192, 32).astype(np.int32)).to(dev)
     us = time_events(lambda i: tree_masks(par, cl), iters, 3)
-    out["config4_tree_masks"] = {"us": round(sum(us) / len(us), 2), "requests": 32, "nodes": 32}
+    out["config4_tree_masks"] = {"us": round(mean(us), 2), "requests": 32, "nodes": 32}
     acc = torch.from_numpy(rng.integers(1, 6, 64).astype(np.int32)).to(dev)
     rej = 25 - acc
     dpt = DevicePageTable(16, 64, 600, dev)
@@ -178,101 +254,153 @@ def extra_configs(dev, iters: int):
         dpt.delete_kv(rej)
     us = time_events(step_dev, iters, 3)
     dpt.check()
-    hpt = PageTable(16, 64, 600, dev)
-    hpt.clear_kv()
-    hpt.insert_kv(torch.from_numpy(rng.integers(1024, 4096, 64).astype(np.int32)).to(dev))
-    for _ in range(3):
-        hpt.insert_kv(25)
-        hpt.delete_kv(rej)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(iters):
-        hpt.insert_kv(25)
-        hpt.delete_kv(rej)
-    torch.cuda.synchronize()
-    host_us = (time.perf_counter() - t0) / iters * 1e6
-    out["page_table_step"] = {"device_us": round(sum(us) / len(us), 2),
-                              "torch_mirror_wall_us": round(host_us, 1), "requests": 64}
+    out["page_table_step"] = {"us": round(mean(us), 2), "requests": 64}
 
-    # the device-side schedule at config 2 (one planner launch per step) and the
-    # attention pass run on it; the host planner's wall time for comparison
-    from batchspec_amd.workloads import config2
-    s2 = [config2(device=dev, seed=1002 + i) for i in range(3)]
     ws2 = [bsx.BatchPrefillWithPagedKVCacheWrapper(torch.empty(256 << 20, dtype=torch.uint8,
-                                                               device=dev), "NHD") for _ in s2]
+                                                               device=dev), "NHD") for _ in sets]
     dev_args = [(b.qo_indptr.to(dev), b.kv_indptr.to(dev), b.kv_indices.to(dev),
-                 b.kv_last_page_len.to(dev)) for b in s2]
+                 b.kv_last_page_len.to(dev)) for b in sets]
 
     def plan_dev(i):
-        b = s2[i % 3]
+        b = sets[i % 3]
         ws2[i % 3].plan(*dev_args[i % 3], b.num_qo_heads, b.num_kv_heads, b.head_dim, b.page_size,
                         causal=True, q_data_type=torch.bfloat16, on_device=True, max_qo_len=5)
     plan_us = time_events(plan_dev, iters, 3)
-    outs2 = [torch.empty_like(b.q) for b in s2]
-    run_us = time_events(lambda i: ws2[i % 3].run(s2[i % 3].q, s2[i % 3].cache, out=outs2[i % 3]),
+    outs2 = [torch.empty_like(b.q) for b in sets]
+    run_us = time_events(lambda i: ws2[i % 3].run(sets[i % 3].q, sets[i % 3].cache, out=outs2[i % 3]),
                          iters, 3)
-    t = sum(run_us) / len(run_us)
-    nb = sum(attn_bytes(b) for b in s2) / 3
+    t = mean(run_us)
+    nb = mean([attn_bytes(b) for b in sets])
     hw = bsx.BatchPrefillWithPagedKVCacheWrapper(torch.empty(256 << 20, dtype=torch.uint8,
                                                              device=dev), "NHD")
-    t0 = time.perf_counter()
+    walls = []
     for i in range(iters):
-        b = s2[i % 3]
-        hw.plan(dev_args[i % 3][0], dev_args[i % 3][1], dev_args[i % 3][2], dev_args[i % 3][3],
-                b.num_qo_heads, b.num_kv_heads, b.head_dim, b.page_size, causal=True,
-                q_data_type=torch.bfloat16)
+        b = sets[i % 3]
+        t0 = time.perf_counter()
+        hw.plan(*dev_args[i % 3], b.num_qo_heads, b.num_kv_heads, b.head_dim, b.page_size,
+                causal=True, q_data_type=torch.bfloat16)
+        walls.append((time.perf_counter() - t0) * 1e6)
     torch.cuda.synchronize()
-    host_plan_us = (time.perf_counter() - t0) / iters * 1e6
-    out["config2_device_plan"] = {"plan_kernel_us": round(sum(plan_us) / len(plan_us), 2),
+    out["config2_device_plan"] = {"plan_kernel_us": round(mean(plan_us), 2),
                                   "attention_us": round(t, 2),
                                   "frac": round(nb / t / 1e3 / HBM_PEAK_GBS, 4),
-                                  "host_plan_wall_us": round(host_plan_us, 1)}
+                                  "host_plan_wall_us_median": round(median(walls), 1)}
+    # accepted-KV compaction (collate_accepted_kv_cache) of the step's accept counts over
+    # three layers of config-2 shape (layers share one page table)
+    kvl = torch.from_numpy(np.ascontiguousarray(sets[0].kv_lens)).to(dev)
+    prev = (kvl - 25).to(torch.int32)
+    caches = [sets[0].cache] + [torch.empty_like(sets[0].cache) for _ in range(2)]
+    col_us = time_events(lambda i: collate_accepted_kv_cache(
+        acc_ref, prev, 4, caches, sets[0].kv_indptr, sets[0].kv_indices), iters, 3)
+    t_col = mean(col_us)
+    moved = int((acc_ref.clamp(max=5) - 1).clamp(min=0).sum()) * 2 * 8 * 128 * 2 * 2 * 3
+    out["collate_accepted_kv"] = {"us_3_layers": round(t_col, 2), "bytes_moved": moved,
+                                  "GB/s": round(moved / t_col / 1e3, 1)}
     return out
 
 
-def cpu_baseline(sets, budget_s: float = 12.0):
-    """fp32 oracle (numpy paged gather + softmax attention) over the config-2 requests,
-    cycling through the batch until about budget_s of CPU work; reported in the
-    metric's unit (GB/s of the same algorithmic bytes)."""
+def cpu_threads() -> int:
+    """Host threads this process may use: the affinity set, capped by OMP_NUM_THREADS
+    when the environment sets it (the GPU box gives one GPU's job a 16-core share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except Exception:
+        n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(b, runs: int = 5):
+    """The reference's CPU path as BASELINE.md defines it: torch fp32 paged gather +
+    scaled_dot_product_attention (bottom-right causal bool mask, GQA) over the whole
+    config-2 batch, on the host's threads; median of `runs` runs after one warmup.
+    Then the C restatement of the stochastic acceptance (oracle/accept.c) over config 5,
+    the requests spread over the same threads."""
     import numpy as np
     import torch
-    from oracle import attention as OA
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:
-        cores = 1
-    b = sets[0]
-    q = b.q.float().cpu().numpy()
+    import torch.nn.functional as F
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
     qo = b.qo_indptr.cpu().numpy()
     kvp = b.kv_indptr.cpu().numpy()
-    idx = b.kv_indices.cpu().numpy()
-    last = b.kv_last_page_len.cpu().numpy()
     lens = b.kv_lens
-    B = len(qo) - 1
-    subs = []
-    for r in range(B):
-        pages = idx[kvp[r]:kvp[r + 1]]
-        sub = b.cache[torch.from_numpy(pages.astype(np.int64)).to(b.cache.device)].float().cpu().numpy()
-        subs.append((pages, sub))
-    t_total, done_bytes, n_req = 0.0, 0, 0
-    while t_total < budget_s:
-        r = n_req % B
-        pages, sub = subs[r]
+    cache = b.cache.float().cpu()
+    idx = b.kv_indices.cpu().long()
+    q = b.q.float().cpu()
+    H, Hkv, D, ps = b.num_qo_heads, b.num_kv_heads, b.head_dim, b.page_size
+
+    def one_pass():
+        out = torch.empty_like(q)
+        for r in range(len(qo) - 1):
+            q0, q1, L = int(qo[r]), int(qo[r + 1]), int(lens[r])
+            pages = idx[int(kvp[r]): int(kvp[r + 1])]
+            kv = cache.index_select(0, pages)  # [n, 2, ps, Hkv, D]
+            K = kv[:, 0].reshape(-1, Hkv, D)[:L].transpose(0, 1)
+            V = kv[:, 1].reshape(-1, Hkv, D)[:L].transpose(0, 1)
+            n_q = q1 - q0
+            mask = torch.arange(L)[None, :] <= (L - n_q + torch.arange(n_q))[:, None]
+            out[q0:q1] = F.scaled_dot_product_attention(
+                q[q0:q1].transpose(0, 1), K, V, attn_mask=mask, enable_gqa=True).transpose(0, 1)
+        return out
+
+    times = []
+    for i in range(runs + 1):
         t0 = time.perf_counter()
-        OA.verify_attention(q[qo[r]:qo[r + 1]], sub, [0, qo[r + 1] - qo[r]],
-                            [0, len(pages)], np.arange(len(pages), dtype=np.int32),
-                            last[r:r + 1], b.page_size, mode="causal")
-        t_total += time.perf_counter() - t0
-        done_bytes += (int(lens[r]) * b.num_kv_heads * b.head_dim * 2 * 2
-                       + 2 * int(qo[r + 1] - qo[r]) * b.num_qo_heads * b.head_dim * 2
-                       + len(pages) * 4)
-        n_req += 1
-    return {"value": round(done_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": int(cores),
-            "kind": "port",
-            "sample": f"{n_req} config-2 requests ({n_req / B:.1f} passes over the batch of {B}), "
-                      f"fp32 numpy paged gather + softmax attention, {t_total:.1f} s of CPU time; "
-                      "bytes counted as the bf16 algorithmic bytes of the GPU metric"}
+        one_pass()
+        times.append(time.perf_counter() - t0)
+    t_attn = median(times[1:])
+    nbytes = attn_bytes(b)
+    rec = {"value": round(nbytes / t_attn / 1e9, 3), "unit": "GB/s", "cores": threads,
+           "kind": "port", "cpu_model": cpu_model(),
+           "sample": f"the whole config-2 batch (64 requests, {nbytes / 1e6:.1f} MB of bf16 "
+                     "algorithmic bytes) through torch fp32 paged gather + "
+                     "scaled_dot_product_attention, median of "
+                     f"{runs} runs after 1 warmup ({t_attn * 1e3:.1f} ms per pass)",
+           "runs_ms": [round(t * 1e3, 1) for t in times[1:]]}
+    del cache
+    # stochastic acceptance, config 5, C restatement, requests spread over the threads
+    from concurrent.futures import ThreadPoolExecutor
+    from batchspec_amd.workloads import stochastic_case
+    from oracle import accept as OAc
+    s = stochastic_case()
+    dl = np.ascontiguousarray(s.draft_logits.float().numpy())
+    tl = np.ascontiguousarray(s.target_logits.float().numpy())
+    ids = s.draft_tokens.numpy()
+    u = s.uniforms.numpy()
+    Bc = tl.shape[0]
+    chunks = [(i, min(Bc, i + max(1, Bc // threads))) for i in range(0, Bc, max(1, Bc // threads))]
+
+    def part(c):
+        return OAc.chain_logits(dl[c[0]:c[1]], ids[c[0]:c[1]], tl[c[0]:c[1]], 1.0, u[c[0]:c[1]])
+    atimes = []
+    with ThreadPoolExecutor(threads) as ex:
+        for i in range(runs + 1):
+            t0 = time.perf_counter()
+            list(ex.map(part, chunks))
+            atimes.append(time.perf_counter() - t0)
+    t_acc = median(atimes[1:])
+    abytes = (tl.size + dl.size) * 2
+    rec["acceptance"] = {"value": round(abytes / t_acc / 1e9, 3), "unit": "GB/s",
+                         "cores": threads, "kind": "port",
+                         "sample": "config 5 (B=128, k=5, V=128256) through the C restatement "
+                                   "of the canonical chain speculative sampling (oracle/accept.c), "
+                                   f"{len(chunks)} request chunks over {threads} threads, median of "
+                                   f"{runs} runs after 1 warmup ({t_acc * 1e3:.0f} ms per batch); "
+                                   "bytes counted as the bf16 logits the GPU path reads",
+                         "runs_ms": [round(t * 1e3, 1) for t in atimes[1:]]}
+    return rec
 
 
 def calibrate_copy(reps: int = 5) -> int:
@@ -282,8 +410,8 @@ def calibrate_copy(reps: int = 5) -> int:
     dst = torch.empty_like(src)
     us = time_events(lambda i: dst.copy_(src), reps, 2)
     print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n,
-                      "us": round(sum(us) / len(us), 2),
-                      "GB/s": round(2 * n / (sum(us) / len(us)) / 1e3, 1)}), flush=True)
+                      "us": round(mean(us), 2), "GB/s": round(2 * n / mean(us) / 1e3, 1)}),
+          flush=True)
     return 0
 
 
@@ -294,9 +422,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-accept", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip configs 4, 3b, 3a and the step plumbing")
+    ap.add_argument("--only", choices=["attn2", "accept", "attn4", "attn3b", "attn3a"],
+                    help="time one part alone (for rocprofv3 counter runs) and print its record")
     ap.add_argument("--calibrate-copy", action="store_true")
-    ap.add_argument("--extra-configs", action="store_true",
-                    help="also time verify attention at configs 4, 3b and 3a")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the "
@@ -304,30 +434,39 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
     if args.calibrate_copy:
         return calibrate_copy()
 
     import batchspec_amd as bsx
-    from batchspec_amd.workloads import config2, greedy_case, stochastic_case
+    from batchspec_amd.workloads import config2
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
-    print("bench: building 3 config-2 input sets on the GPU", file=sys.stderr, flush=True)
+    if args.only and args.only != "attn2":
+        rec = {}
+        if args.only == "accept":
+            acceptance(dev, args.steps, rec)
+        elif args.only == "attn4":
+            rec["config4_tree_attention"] = config4_attention(dev, args.steps)
+        elif args.only == "attn3b":
+            rec["config3b_verify_attention"] = config3b_attention(dev, args.steps)
+        else:
+            rec["config3a_draft_attention"] = config3a_attention(dev, args.steps)
+        print(json.dumps(rec), flush=True)
+        return 0
+
+    log("building 3 config-2 input sets on the GPU")
     sets = [config2(device=dev, seed=1002 + i) for i in range(3)]
-    ws = [torch.empty(256 << 20, dtype=torch.uint8, device=dev) for _ in sets]
-    wrappers = []
-    plan_us = []
-    for b, w_buf in zip(sets, ws):
-        w = bsx.BatchPrefillWithPagedKVCacheWrapper(w_buf, "NHD")
-        t0 = time.perf_counter()
+    wrappers, outs = [], []
+    for b in sets:
+        w = bsx.BatchPrefillWithPagedKVCacheWrapper(
+            torch.empty(256 << 20, dtype=torch.uint8, device=dev), "NHD")
         w.plan(b.qo_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, b.num_qo_heads,
                b.num_kv_heads, b.head_dim, b.page_size, causal=True, q_data_type=torch.bfloat16)
-        plan_us.append((time.perf_counter() - t0) * 1e6)
         wrappers.append(w)
-    outs = [torch.empty_like(b.q) for b in sets]
+        outs.append(torch.empty_like(b.q))
     abytes = [attn_bytes(b) for b in sets]
     pbytes = [append_bytes(b) for b in sets]
 
@@ -340,7 +479,7 @@ def main() -> int:
 
     # --- timed steps (append + attention): barrier-free single GPU, synchronize on both
     # sides of exactly `steps` steps
-    print(f"bench: {args.warmup} warmup + {args.steps} timed steps", file=sys.stderr, flush=True)
+    log(f"{args.warmup} warmup + {args.steps} timed steps")
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -362,11 +501,11 @@ def main() -> int:
                                                  sets[i % 3].qo_indptr, sets[i % 3].cache,
                                                  sets[i % 3].kv_indptr, sets[i % 3].kv_indices,
                                                  sets[i % 3].kv_last_page_len), args.steps, 3)
-    t_attn = sum(attn_us) / len(attn_us)
-    t_app = sum(app_us) / len(app_us)
-    a_bytes = sum(abytes) / 3
+    t_attn, t_app = mean(attn_us), mean(app_us)
+    a_bytes = mean(abytes)
     achieved = a_bytes / (t_attn * 1e-6) / 1e9
     p0 = wrappers[0].plan_info
+    mfma = profile_value(MFMA_FILE, "mfma_util_config2")
     result = {
         "metric": METRIC,
         "value": round(achieved, 1),
@@ -390,80 +529,53 @@ def main() -> int:
         "attn_us": round(t_attn, 2),
         "attn_us_median": round(median(attn_us), 2),
         "append_us": round(t_app, 2),
-        "append_GBs": round(sum(pbytes) / 3 / t_app / 1e3, 1),
+        "append_GBs": round(mean(pbytes) / t_app / 1e3, 1),
         "attn_bytes": int(a_bytes),
-        "plan_us": round(median(plan_us), 1),
         "plan": {"workgroups": int(p0.num_ctas), "segments": int(p0.num_segments),
                  "split_requests": int(p0.num_split_requests), "tiles": int(p0.total_tiles)},
         "wall_s": round(wall, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(),
+                     "traffic": profile_value(TRAFFIC_FILE, "traffic_bytes_per_pass"),
+                     "mfma_util": mfma,
                      "kernel": "verify attention pass (verify_attn_kernel + merge_kernel)"},
     }
+    if args.only == "attn2":
+        print(json.dumps(result), flush=True)
+        return 0
 
+    t_acc = None
     if not args.skip_accept:
-        # greedy acceptance at the config-2 shape: fused argmax over [64, 5, 128256] bf16
-        g = greedy_case(B=64, k=4, V=128256, p_match=0.7, seed=2002, dtype=torch.bfloat16)
-        gl, gd = g.target_logits.to(dev), g.draft_tokens.to(dev)
-        acc_us = time_events(lambda i: bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1),
-                             args.steps, 3)
-        _, acc_ref, _ = bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1)
-        _, acc_pre, _ = bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1,
-                                               accept_rule="prefix")
-        t_acc = sum(acc_us) / len(acc_us)
-        t_model = 32 * (t_attn + t_app) + t_acc
-        n_ref, n_pre = int(acc_ref.sum()), int(acc_pre.sum())
-        result["accepted_tok_s"] = round(n_ref / (t_model * 1e-6), 1)
-        result["accepted_tok_s_prefix_rule"] = round(n_pre / (t_model * 1e-6), 1)
-        result["mean_accept_len"] = {"reference_rule": n_ref / 64, "prefix_rule": n_pre / 64}
-        gbytes = gl.numel() * 2
-        result["greedy_accept"] = {"us": round(t_acc, 2), "GB/s": round(gbytes / t_acc / 1e3, 1),
-                                   "frac": round(gbytes / t_acc / 1e3 / HBM_PEAK_GBS, 4)}
-        result["verify_step_32_layers_us"] = round(t_model, 1)
-        # accepted-KV compaction (collate_accepted_kv_cache) of the same accept counts over
-        # three layers of config-2 shape (set 0's cache and two more of its shape; layers
-        # share one page table): rows prev + i*(k+1) -> prev + i
-        from batchspec_amd.collate import collate_accepted_kv_cache
-        kvl = torch.from_numpy(np.ascontiguousarray(sets[0].kv_lens)).to(dev)
-        prev = (kvl - 25).to(torch.int32)
-        caches = [sets[0].cache] + [torch.empty_like(sets[0].cache) for _ in range(2)]
-        col_us = time_events(lambda i: collate_accepted_kv_cache(
-            acc_ref, prev, 4, caches, sets[0].kv_indptr, sets[0].kv_indices), args.steps, 3)
-        t_col = sum(col_us) / len(col_us)
-        moved = int((acc_ref.clamp(max=5) - 1).clamp(min=0).sum()) * 2 * 8 * 128 * 2 * 2 * 3
-        result["collate_accepted_kv"] = {"us_3_layers": round(t_col, 2),
-                                         "bytes_moved": moved,
-                                         "GB/s": round(moved / t_col / 1e3, 1)}
-        del gl, g, caches
-        # stochastic acceptance (config 5)
-        s = stochastic_case(device=dev)
-        st_us = time_events(lambda i: bsx.sampling.chain_speculative_sampling_from_logits(
-            s.draft_logits, s.draft_tokens, s.target_logits, 1.0, uniforms=s.uniforms),
-            max(5, args.steps // 3), 2)
-        t_st = sum(st_us) / len(st_us)
-        sbytes = (s.target_logits.numel() + s.draft_logits.numel()) * 2
-        result["stochastic_accept"] = {"us": round(t_st, 2), "GB/s": round(sbytes / t_st / 1e3, 1),
-                                       "frac": round(sbytes / t_st / 1e3 / HBM_PEAK_GBS, 4),
-                                       "bytes": sbytes}
-        # the same acceptance with the reference's default filters (top_k=20, top_p=0.95)
-        # applied to both distributions
-        sf_us = time_events(lambda i: bsx.sampling.chain_speculative_sampling_from_logits(
-            s.draft_logits, s.draft_tokens, s.target_logits, 1.0, uniforms=s.uniforms,
-            top_k=20, top_p=0.95), max(5, args.steps // 3), 2)
-        t_sf = sum(sf_us) / len(sf_us)
-        result["stochastic_accept_top_k20_top_p095"] = {
-            "us": round(t_sf, 2), "GB/s": round(sbytes / t_sf / 1e3, 1),
-            "frac": round(sbytes / t_sf / 1e3 / HBM_PEAK_GBS, 4), "bytes": sbytes}
-        del s
+        log("acceptance: greedy [64,5,128256], stochastic config 5")
+        t_acc, acc_ref, acc_pre = acceptance(dev, args.steps, result)
 
-    if args.extra_configs:
-        print("bench: configs 4, 3b, 3a", file=sys.stderr, flush=True)
-        result.update(extra_configs(dev, args.steps))
+    if not args.no_extra:
+        log("verify attention at configs 4, 3b, 3a")
+        result["config4_tree_attention"] = config4_attention(dev, args.steps)
+        result["config3b_verify_attention"] = config3b_attention(dev, args.steps)
+        result["config3a_draft_attention"] = config3a_attention(dev, args.steps)
+        if t_acc is not None:
+            log("step plumbing: page table, device plan, tree masks, compaction")
+            plumbing = step_plumbing(dev, args.steps, sets, acc_ref)
+            result.update(plumbing)
+            t_plan = plumbing["config2_device_plan"]["plan_kernel_us"]
+            t_pt = plumbing["page_table_step"]["us"]
+            t_host = plumbing["config2_device_plan"]["host_plan_wall_us_median"]
+            t_model = t_pt + t_plan + NUM_LAYERS * (t_attn + t_app) + t_acc
+            n_ref, n_pre = int(acc_ref.sum()), int(acc_pre.sum())
+            result["accepted_tok_s"] = round(n_ref / (t_model * 1e-6), 1)
+            result["accepted_tok_s_prefix_rule"] = round(n_pre / (t_model * 1e-6), 1)
+            result["accepted_tok_s_host_plan"] = round(
+                n_ref / ((t_model - t_plan + t_host) * 1e-6), 1)
+            result["mean_accept_len"] = {"reference_rule": n_ref / 64, "prefix_rule": n_pre / 64}
+            result["verify_step_us"] = {
+                "total": round(t_model, 1), "page_table": t_pt, "device_plan": t_plan,
+                "layers_attention_append": round(NUM_LAYERS * (t_attn + t_app), 1),
+                "greedy_accept": round(t_acc, 2), "layers": NUM_LAYERS}
 
     if not args.no_cpu_baseline:
-        print("bench: CPU baseline (fp32 oracle, ~12 s)", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(sets)
+        log("CPU baseline: torch fp32 SDPA over config 2, C acceptance over config 5")
+        result["cpu_baseline"] = cpu_baseline(sets[0])
     print(json.dumps(result), flush=True)
     return 0
 
