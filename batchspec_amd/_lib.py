@@ -19,6 +19,8 @@ BSX_ERR_CAPACITY = -2
 BSX_ERR_UNSUPPORTED = -3
 BSX_ERR_HIP = -4
 
+NOALLOC_SCRATCH_BYTES = 4 << 20  # BSX_NOALLOC_SCRATCH_BYTES of include/bsx.h
+
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
 DTYPE_FP32 = 2
@@ -100,6 +102,8 @@ SIGNATURES = {
     "bsx_accept_greedy_ws_bytes": (c_int64, [c_int, c_int, c_int64]),
     "bsx_accept_greedy": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int64, c_int64, c_int, _P, _P,
                                   _P, _P, c_int64, _P]),
+    "bsx_accept_greedy_noalloc": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int64, c_int64, c_int,
+                                          _P, _P, _P, _P]),
     "bsx_chain_ws_bytes": (c_int64, [c_int, c_int, c_int64]),
     "bsx_chain_speculative_sampling": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int64, _P, _P, _P,
                                                _P, c_int64, _P]),

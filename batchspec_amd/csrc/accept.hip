@@ -22,6 +22,7 @@
 // This translation unit is compiled with -ffp-contract=off: every multiply-add
 // that the canonical order fuses is an explicit fmaf.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 #include "canon.h"
@@ -782,6 +783,59 @@ extern "C" int bsx_accept_greedy(const int64_t* draft_d, const int64_t* target_i
                      accept_d, eos_acc_d);
   BSX_LAUNCH_CHECK();
   return BSX_OK;
+}
+
+// ---- greedy acceptance without a caller workspace ----------------------------------
+// The argmax partials live in a file-scope device array (one copy per GPU, held until
+// the process ends).  Host code never passes the array's name to a kernel: its device
+// address is looked up once per device with hipGetSymbolAddress, with that device
+// current, and kept in g_scratch_addr.  Calls on one GPU share the array, so calls
+// that overlap in time on one GPU (different streams without ordering) race; the
+// partials are fully written before they are read, so nothing in it must start at zero.
+namespace {
+constexpr int kMaxScratchDevices = 64;
+__device__ __align__(256) unsigned char scratch[BSX_NOALLOC_SCRATCH_BYTES];
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxScratchDevices];
+}  // namespace
+
+static int scratch_address(void** out) {
+  int dev = -1;
+  BSX_HIP_CHECK(hipGetDevice(&dev));
+  BSX_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, BSX_ERR_UNSUPPORTED,
+              "device %d beyond the %d devices the allocation-free scratch supports", dev,
+              kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    BSX_REQUIRE(e == hipSuccess && p != nullptr, BSX_ERR_HIP,
+                "hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return BSX_OK;
+}
+
+extern "C" int bsx_accept_greedy_noalloc(const int64_t* draft_d, const int64_t* target_ids_d,
+                                         const void* target_logits_d, int dtype, int B, int k,
+                                         int64_t vocab, int64_t eos_id, int mode,
+                                         int64_t* bonus_d, int64_t* accept_d,
+                                         uint8_t* eos_acc_d, void* stream) {
+  if (target_ids_d == nullptr && B > 0 && k >= 0 && vocab > 0) {
+    const int64_t need = bsx_accept_greedy_ws_bytes(B, k, vocab);
+    BSX_REQUIRE(need <= (int64_t)BSX_NOALLOC_SCRATCH_BYTES, BSX_ERR_CAPACITY,
+                "B=%d k=%d vocab=%lld needs %lld bytes of argmax partials; the "
+                "allocation-free scratch holds %lld (use bsx_accept_greedy with a workspace)",
+                B, k, (long long)vocab, (long long)need, (long long)BSX_NOALLOC_SCRATCH_BYTES);
+  }
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != BSX_OK) return rc;
+  return bsx_accept_greedy(draft_d, target_ids_d, target_logits_d, dtype, B, k, vocab, eos_id,
+                           mode, bonus_d, accept_d, eos_acc_d, ws,
+                           (int64_t)BSX_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 static int64_t chain_ws_layout(int B, int k, int64_t V, bool logits, int64_t* off_lanes,

@@ -276,6 +276,21 @@ int bsx_accept_greedy(const int64_t* draft_d, const int64_t* target_ids_d,
                       int64_t* accept_d, uint8_t* eos_acc_d, void* ws_d,
                       int64_t ws_bytes, void* stream);
 
+/* Allocation-free greedy acceptance: no counterpart in the reference.  For callers
+ * that cannot allocate or pass a workspace (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results as
+ * bsx_accept_greedy without ws_d / ws_bytes: the argmax partials go to a file-scope
+ * device array of BSX_NOALLOC_SCRATCH_BYTES bytes per GPU, held until the process
+ * ends.  Shapes whose partials exceed it (bsx_accept_greedy_ws_bytes(B, k, vocab) >
+ * BSX_NOALLOC_SCRATCH_BYTES; at vocab 128256 in bf16 that is B*(k+1) > 131072 rows)
+ * return BSX_ERR_CAPACITY.  The library allocates nothing here.  Every call on a GPU
+ * shares that GPU's array: calls that overlap in time on one GPU race. */
+#define BSX_NOALLOC_SCRATCH_BYTES (4 << 20)
+int bsx_accept_greedy_noalloc(const int64_t* draft_d, const int64_t* target_ids_d,
+                              const void* target_logits_d, int dtype, int B, int k,
+                              int64_t vocab, int64_t eos_id, int mode, int64_t* bonus_d,
+                              int64_t* accept_d, uint8_t* eos_acc_d, void* stream);
+
 /* Chain speculative sampling (flashinfer.sampling.chain_speculative_sampling as
  * called at batchspec/backends/mtp_engine.py:569) with explicit uniforms.
  *   draft_probs_d [B,k,V] fp32 or NULL (NULL = one-hot at the draft token, the
