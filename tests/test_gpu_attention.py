@@ -382,6 +382,35 @@ def test_config3b_plain_inputs_normalised():
     AP.assert_discriminates(ref, [("zeros", np.zeros_like(ref[0]), None)])
 
 
+def test_split_partials_against_an_unsplit_run():
+    """What storing split-KV partials in the input dtype costs: config 3b's plain inputs
+    (4 requests of 32k-64k tokens) on the default plan, every request split and merged,
+    against a one-workgroup plan that splits nothing; both against the oracle."""
+    say("config 3b plain inputs, 4 requests: split plan vs unsplit plan")
+    b = config3(device=DEV, batch=4)
+    w = _host_plan_run(b)
+    assert w.plan_info.num_split_requests == 4
+    split, _ = _run(w, b)
+    w1 = bsx.BatchPrefillWithPagedKVCacheWrapper(torch.empty(64 << 20, dtype=torch.uint8,
+                                                             device=DEV), "NHD")
+    w1._num_cus = 1  # a persistent grid of one workgroup: no request is split
+    w1.plan(b.qo_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, b.num_qo_heads,
+            b.num_kv_heads, b.head_dim, b.page_size, causal=True, q_data_type=b.q.dtype)
+    assert w1.plan_info.num_ctas == 1 and w1.plan_info.num_split_requests == 0
+    whole, _ = _run(w1, b)
+    ref = AP.oracle_per_request(b, "causal")[None]
+    m = float(np.abs(ref[0]).max())
+    d = (split.float() - whole.float()).abs().max().item()
+    e_split = float(np.abs(split.float().cpu().numpy() - ref[0]).max())
+    e_whole = float(np.abs(whole.float().cpu().numpy() - ref[0]).max())
+    say(f"  max|ref| {m:.3g}; max|split - unsplit| {d:.3g} ({d / m:.3%}); vs oracle: "
+        f"split {e_split / m:.3%}, unsplit {e_whole / m:.3%}; "
+        f"{w.plan_info.num_segments} segments")
+    AP.check(split, ref[0])
+    AP.check(whole, ref[0])
+    assert d <= 1e-2 * m
+
+
 def test_config3a_sink_window_full_size():
     """Config 3a (B=32, one query over a 64-sink + 512-window view of 32k-64k tokens)
     with planted keys at the view's edges; guards: sink or window off by one/32."""
