@@ -275,7 +275,8 @@ __device__ __forceinline__ void pv_tile(const u32x4 (&va)[NJ], const uint32_t (&
 }
 
 // End of a segment: normalise and store the wave's rows as the request's output, or,
-// for a split request, as a bf16 partial with its log2-sum-exp for the merge kernel.
+// for a split request, as a partial in the input dtype with its log2-sum-exp for the
+// merge kernel.
 // Lane (c16, g4) holds row c16 of tile nt at d = NJ*(4 g4 + e) + jm (INTERLEAVED,
 // 4 NJ consecutive values per lane) or at d = 16 jm + 4 g4 + e (runs of 4).
 template <int DT, int D, int NT, bool INTERLEAVED>
@@ -686,7 +687,7 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
   constexpr int NPER = L::kChunks / QB;  // direct loads per wave per tile
   constexpr int WAIT = (S - 2) * NPER;
   constexpr int HALF_CHUNKS = L::kChunks / 2;
-  static_assert(L::kChunks % QB == 0 && (S & (S - 1)) == 0, "bad shared-tile shape");
+  static_assert(L::kChunks % QB == 0 && (S & (S - 1)) == 0 && S <= 4, "bad shared-tile shape");
 
   __shared__ __attribute__((aligned(1024))) u32x4 smem[attn_shape::shared_lds_bytes(D, QB) / 16];
 
@@ -728,6 +729,7 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
   // The page ids are read when the cursor moves, one tile before the loads that use
   // them: a scalar read issued right before the loads would put its latency (long
   // under full memory load) on every tile's critical path.
+  int pr_count = 0;  // tiles whose loads were issued
   int pr_si = seg_begin, pr_tile = 0, pr_t1 = 0, pr_kv = 0, pr_pages = 0;
   int pr_page0 = 0, pr_page1 = 0;  // (scalars, not an array indexed by a
   int pr_pofs0 = 0, pr_pofs1 = 0;  //  wave-dependent subtile: no dynamic indexing)
@@ -767,6 +769,7 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
   };
   auto pr_issue = [&](int stage) {
     if (!pr_valid) return;
+    ++pr_count;
     const uint32_t lds_stage =
         lds_base + (uint32_t)((stage * stage_granules) * 16 + hs * L::kHeadBytes);
 #pragma unroll
@@ -810,6 +813,20 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
     vtr[jm] = 2 * L::at(4 * g4 + (c16 >> 2), 2 * jm + ((c16 & 3) >> 1)) + (c16 & 1);
 
   int n = 0;  // tiles consumed so far (stage n mod S)
+  // Wait until this wave's loads of tile n landed: loads return in issue order, so it
+  // is enough that no more than the loads of the tiles issued after it are still in
+  // flight (S-2 tiles in the steady state; fewer at the end of the schedule, where no
+  // tile follows).
+  auto wait_tile = [&]() {
+    const int younger = pr_count - n - 1;
+    if (younger >= S - 2) {
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(WAIT) : "memory");
+    } else if (S >= 4 && younger == 1) {
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(NPER) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    }
+  };
   for (int si = seg_begin; si < seg_end; ++si) {
     const Seg cur = load_seg(p, si);
     const int nrows = cur.qo_len * g;
@@ -865,7 +882,7 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
       constexpr bool MASKED = decltype(masked_tag)::value;
       const int j0 = tile * kTile;
       const int stage = n & (S - 1);
-      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(WAIT) : "memory");
+      wait_tile();
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       pr_issue((stage + S - 1) & (S - 1));
