@@ -19,7 +19,10 @@ Printed: one JSON line with
   greedy_accept / stochastic_accept   acceptance at [64, 5, 128256] (config-2 shape)
               and config 5 (B=128, k=5, V=128256), time and HBM fraction
   config4_tree_attention / config3b_verify_attention / config3a_draft_attention
-              verify attention at the other BASELINE configurations
+              verify attention at the other BASELINE configurations (config 4 also
+              `spaced`: the same runs separated by short idle gaps, which keep the
+              shader clock unthrottled; back-to-back it settles lower under the power
+              limit)
   accepted_tok_s  accepted tokens/s of a 32-layer verify step: the page-table update
               (insert + delete), one device plan, 32 x (append + attention) and the
               fused greedy acceptance over [64, 5, 128256] bf16 logits (draft = target
@@ -150,11 +153,36 @@ def pass_record(wr, us, nbytes):
                      "waves_per_head": int(p.qblocks_per_cta)}}
 
 
+def spaced_runs(wr, sets, iters, gap_cycles=400_000):
+    """Mean GPU time of runs separated by short idle gaps (a GPU sleep of about 0.2 ms
+    before each): the shader clock stays at its unthrottled rate between such runs,
+    while back-to-back runs of a matrix-core-heavy kernel settle at a lower clock under
+    the board's power limit."""
+    import torch
+    outs = [torch.empty_like(b.q) for b in sets]
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(iters)]
+    torch.cuda._sleep(50_000_000)
+    for i in range(iters):
+        j = i % len(sets)
+        torch.cuda._sleep(gap_cycles)
+        ev[i][0].record()
+        wr[j].run(sets[j].q, sets[j].cache, out=outs[j])
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) * 1e3 for a, b in ev]
+
+
 def config4_attention(dev, iters):
     from batchspec_amd.workloads import config4
     s4 = [config4(device=dev, seed=1004 + i) for i in range(3)]
     wr, us = attention_pass(dev, s4, dict(causal=False, tree=True), iters)
-    rec = pass_record(wr, us, mean([attn_bytes(b) for b in s4]))
+    nbytes = mean([attn_bytes(b) for b in s4])
+    rec = pass_record(wr, us, nbytes)
+    sp = mean(spaced_runs(wr, s4, iters))
+    rec["spaced"] = {"us": round(sp, 2), "frac": round(nbytes / sp / 1e3 / HBM_PEAK_GBS, 4),
+                     "note": "runs separated by ~0.2 ms idle gaps (unthrottled shader clock); "
+                             "`us` above is back-to-back, the bench's measure"}
     rec["workload"] = "B=32, ctx U[2048,8192], 32-node draft trees (ancestor bitmask), 32/8 heads"
     return rec
 
