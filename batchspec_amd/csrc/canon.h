@@ -3,12 +3,14 @@
 // Acceptance must give bit-identical token ids on the GPU and on a CPU restatement
 // fed the same uniforms.  That requires every floating-point value the decisions
 // depend on to be produced by the same sequence of IEEE-754 binary32 operations:
-//   * exp is our own: 2^y = 2^n * P(f), n = floor(y), f = fl(y - n) capped at the
-//     largest float below 1 (the GPU's v_fract_f32 and v_cvt_flr_i32_f32), P a
-//     degree-5 polynomial with P(0) = 1 fitted to 2^f on [0, 1) for relative error
-//     (Lawson iteration, coefficients rounded to binary32 and tuned in the last bit),
-//     evaluated by Horner with fused multiply-add; at most 3 ulp from 2^y.
-//     Arguments below -200 are clamped (2^-200 underflows to 0 in ldexp).
+//   * exp is our own: 2^y = ldexp(P(f), n), n = floor(y) saturated to the int32 range,
+//     f = fl(y - n) capped at the largest float below 1 (the GPU's v_cvt_flr_i32_f32
+//     and v_fract_f32, the latter with its clamp modifier, so that f = 0 for an
+//     infinite y), P a degree-5 polynomial with P(0) = 1 fitted to 2^f on [0, 1) for
+//     relative error (Lawson iteration, coefficients rounded to binary32 and tuned in
+//     the last bit), evaluated by Horner with fused multiply-add; at most 3 ulp from
+//     2^y.  exp2(-inf) = 0 (n = INT_MIN); arguments far below -150 underflow to 0 in
+//     ldexp without a clamp.
 //   * every sum runs over a fixed tree, independent of the launch configuration:
 //       - a row of V values is cut into groups of 8 consecutive elements
 //         (group g = elements [8g, 8g+8) ∩ [0, V));
@@ -20,12 +22,15 @@
 //         (node = left child + right child).
 //   * softmax statistics use the same lanes with an online maximum.  A lane keeps
 //     its running max m and the reference rho(m) = fl(m·C), C = log2(e) * (1/T);
-//     its elements are weighted 2^fma(x, C, -rho(m)).  When a group max gm exceeds
-//     m: s *= 2^(rho(m) - rho(gm)) and m = gm; then s += the group sum of weights.
+//     its elements are weighted 2^fma(x, C, -rho(m)), with rho(-inf) taken as 0 (a
+//     lane that has only seen -inf so far weighs its -inf elements 2^-inf = 0).  When
+//     a group max gm exceeds m: s *= 2^(rho(m) - rho(gm)) and m = gm; then s += the
+//     group sum of weights.
 //     The row max M is the max over lanes; the row sum Z is the binary tree over
 //     lanes of s_lane·2^(rho(m_lane) - rho(M)) (each lane rescaled exactly once).
 //     Later weights are 2^fma(x, C, -rho(M)).
-// Inputs are finite (a row needs at least one finite logit).
+// Inputs are finite or -inf (a row needs at least one finite logit), with |x * C| below
+// 2^127 for finite x.
 #pragma once
 
 #include <math.h>
@@ -55,15 +60,22 @@ constexpr float kC4 = 0x1.277854p-7f;
 constexpr float kC5 = 0x1.e974f6p-10f;
 
 BSX_HD float exp2(float y) {
-  y = fmaxf(y, -200.0f);
 #ifdef __HIP_DEVICE_COMPILE__
-  const float f = __builtin_amdgcn_fractf(y);
+  float f;
+  asm("v_fract_f32_e64 %0, %1 clamp" : "=v"(f) : "v"(y));
   int n;
   asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(n) : "v"(y));
 #else
-  const float fl = floorf(y);
-  const float f = fminf(y - fl, 0x1.fffffep-1f);
-  const int n = (int)fl;
+  float f;
+  int n;
+  if (y != y) {
+    f = 0.0f;
+    n = INT32_MAX;
+  } else {
+    const float fl = floorf(y);
+    f = fl == y ? 0.0f : fminf(y - fl, 0x1.fffffep-1f);
+    n = fl >= 0x1p31f ? INT32_MAX : (fl < -0x1p31f ? INT32_MIN : (int)fl);
+  }
 #endif
   float p = kC5;
   p = fmaf(p, f, kC4);
@@ -83,6 +95,9 @@ BSX_HD float scale_for_temperature(float temperature) {
 // Weight of a logit relative to the row max: 2^(fma(x, C, -(M*C))).
 BSX_HD float weight(float x, float c, float neg_mc) { return exp2(fmaf(x, c, neg_mc)); }
 
+// -rho(m) of a lane's running max m: -(m*C), and 0 while m is -inf.
+BSX_HD float neg_ref(float m, float c) { return m == -INFINITY ? 0.0f : -(m * c); }
+
 // Online lane state: running max m (reference rho = m*C) and weight sum s.
 struct LaneState {
   float m;
@@ -95,7 +110,7 @@ BSX_HD void lane_update(LaneState& st, const float* x, int n, float gm, float c)
     st.s = st.s * exp2(st.m * c - gm * c);
     st.m = gm;
   }
-  const float neg_rho = -(st.m * c);
+  const float neg_rho = neg_ref(st.m, c);
   float gs = 0.f;
   for (int e = 0; e < n; ++e) gs = gs + weight(x[e], c, neg_rho);
   st.s = st.s + gs;

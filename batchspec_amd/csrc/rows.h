@@ -137,7 +137,7 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float neg_rho = -(st[i].m * c);
+        const float neg_rho = canon::neg_ref(st[i].m, c);
         // = 0 + w0 + ... exactly: weights are >= +0
         float gs = canon::weight(x[i][0], c, neg_rho);
 #pragma unroll

@@ -14,14 +14,15 @@
  *
  * Floating-point values follow the deterministic ("canonical") order the GPU kernels
  * document, restated here from that specification:
- *   exp2(y): y = max(y, -200); n = floor(y); f = min(fl(y - n), largest float < 1);
- *            P(f) = Horner-fma of the degree-5 polynomial with P(0) = 1 fitted to
- *            2^f on [0, 1) for relative error (binary32 coefficients below);
- *            ldexp(P, n).
+ *   exp2(y): n = floor(y) saturated to int32 (NaN: INT32_MAX); f = min(fl(y - n),
+ *            largest float < 1), 0 for an infinite or NaN y; P(f) = Horner-fma of
+ *            the degree-5 polynomial with P(0) = 1 fitted to 2^f on [0, 1) for
+ *            relative error (binary32 coefficients below); ldexp(P, n).
  *   weights: w(x) = exp2(fma(x, C, -(M*C))), C = log2(e) * (1/T).
  *   groups of 8 consecutive elements; lane (8t+i) owns groups t + 256*i + 2048*j.
- *   row stats: per lane, running max m with reference fl(m*C) (rescale on a new max),
- *   then every lane rescaled once to the row max and summed by the tree over lanes.
+ *   row stats: per lane, running max m with reference fl(m*C) (0 while m = -inf;
+ *   rescale on a new max), then every lane rescaled once to the row max and summed by
+ *   the tree over lanes.
  *   sums: group sums left to right, lane sums over groups in j order, balanced tree
  *   over lanes; draws walk down that tree.
  * Build: cc -O2 -ffp-contract=off -fPIC -shared (see oracle/build.py).
@@ -40,13 +41,20 @@ static const float POLY[6] = {0x1.0p+0f,      0x1.62e4bap-1f, 0x1.ebdb5ap-3f,
                               0x1.c91ce4p-5f, 0x1.277854p-7f, 0x1.e974f6p-10f};
 
 float oc_exp2(float y) {
-  if (y < -200.0f || y != y) y = -200.0f; /* fmaxf(y, -200): NaN -> -200 */
-  float fl = floorf(y);
-  float f = y - fl;
-  if (f > 0x1.fffffep-1f) f = 0x1.fffffep-1f; /* fract is below 1 */
+  float f;
+  int n;
+  if (y != y) { /* the GPU's clamped fract gives 0, its floor conversion INT32_MAX */
+    f = 0.0f;
+    n = INT32_MAX;
+  } else {
+    const float fl = floorf(y);
+    f = fl == y ? 0.0f : y - fl; /* 0 for an integer or infinite y */
+    if (f > 0x1.fffffep-1f) f = 0x1.fffffep-1f; /* fract is below 1 */
+    n = fl >= 0x1p31f ? INT32_MAX : (fl < -0x1p31f ? INT32_MIN : (int)fl);
+  }
   float p = POLY[5];
   for (int i = 4; i >= 0; --i) p = fmaf(p, f, POLY[i]);
-  return ldexpf(p, (int)fl);
+  return ldexpf(p, n);
 }
 
 static float weight(float x, float c, float neg_mc) { return oc_exp2(fmaf(x, c, neg_mc)); }
@@ -83,7 +91,7 @@ void oc_row_stats(const float* x, int64_t V, float c, float* M, float* Z) {
         s = s * oc_exp2(m * c - gm * c);
         m = gm;
       }
-      float neg = -(m * c);
+      float neg = m == -INFINITY ? 0.0f : -(m * c);
       float gs = 0.0f;
       for (int e = 0; e < n; ++e) gs = gs + weight(x[v0 + e], c, neg);
       s = s + gs;

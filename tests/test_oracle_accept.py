@@ -21,7 +21,10 @@ def test_exp2_within_three_ulp_of_libm(oracle_lib):
     assert A.exp2(0.0) == 1.0
     assert A.exp2(-1.0) == 0.5
     assert A.exp2(-300.0) == 0.0
-    assert A.exp2(float("nan")) == 0.0
+    # no clamp: far below the float range, beyond int32 and -inf all underflow to 0
+    assert A.exp2(-1e30) == 0.0 and A.exp2(-3e9) == 0.0 and A.exp2(float("-inf")) == 0.0
+    # denormal results round like ldexp
+    assert A.exp2(-149.0) == 2.0 ** -149 and A.exp2(-127.5) == float(np.float32(2.0 ** -127.5))
 
 
 @pytest.mark.parametrize("T", [1.0, 0.6, 1.7])
