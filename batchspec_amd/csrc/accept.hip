@@ -64,6 +64,7 @@ struct ChainArgs {
   int64_t V;
   float* lanes;  // [B, 2048]
   float* gsum;   // [B, G]
+  int32_t* dec;  // [B, 2]: the residual kernel's decision (j, independent accepts)
   int32_t* out_ids;
   int32_t* accepted;
   int32_t* emitted;
@@ -127,10 +128,23 @@ struct Chain {
 
   // j (first rejected position, k if none) and the independent accept count, for the
   // whole workgroup: the first wave runs the k ratio tests in parallel (lane i, test i).
-  __device__ __forceinline__ int decide(int b, int* n_accept) const {
+  // With k < 64 (LOGITS), lane i also reads the statistics of target row i and draft
+  // row i up front, and the lane of row j hands them to the workgroup (pre_*), so the
+  // residual's first loads do not wait for another round trip.
+  bool pre = false;
+  float2 pre_ts, pre_ds;
+
+  __device__ __forceinline__ int decide(int b, int* n_accept) {
     __shared__ int s_j, s_n;
+    __shared__ float2 s_ts, s_ds;
+    const bool stage = LOGITS && a.k < 64;
     if (threadIdx.x < 64) {
       const int lane = threadIdx.x;
+      float2 ts = {0.f, 0.f}, ds = {0.f, 0.f};
+      if (stage && lane <= a.k) {
+        ts = tstat(b, lane);
+        if (lane < a.k && has_draft_dist()) ds = dstat(b, lane);
+      }
       int j = a.k, cnt = 0;
       for (int i0 = 0; i0 < a.k; i0 += 64) {
         const int i = i0 + lane;
@@ -144,9 +158,18 @@ struct Chain {
         s_j = j;
         s_n = cnt;
       }
+      if (stage && lane == j) {
+        s_ts = ts;
+        s_ds = ds;
+      }
     }
     __syncthreads();
     *n_accept = s_n;
+    if (stage) {
+      pre = true;
+      pre_ts = s_ts;
+      pre_ds = s_ds;
+    }
     return s_j;
   }
 
@@ -174,11 +197,11 @@ struct Chain {
     rr.dvec = (((uintptr_t)rr.dr) % 16 == 0) && ((V * esz) % 16 == 0);
     rr.tnmc = rr.tinv = rr.dnmc = rr.dinv = 0.f;
     if constexpr (LOGITS) {
-      const float2 ts = tstat(b, j);
+      const float2 ts = pre ? pre_ts : tstat(b, j);
       rr.tnmc = -(ts.x * a.c);
       rr.tinv = 1.0f / ts.y;
       if (rr.with_q && rr.dist) {
-        const float2 ds = dstat(b, j);
+        const float2 ds = pre ? pre_ds : dstat(b, j);
         rr.dnmc = -(ds.x * a.c);
         rr.dinv = 1.0f / ds.y;
       }
@@ -257,6 +280,10 @@ __global__ void __launch_bounds__(256) residual_kernel(ChainArgs a) {
   const int w = blockIdx.y;
   int nacc;
   const int j = ch.decide(b, &nacc);
+  if (w == 0 && threadIdx.x == 0) {  // for the pick kernel
+    a.dec[2 * b] = j;
+    a.dec[2 * b + 1] = nacc;
+  }
   const int lam = 8 * threadIdx.x + w;
   a.lanes[(int64_t)b * kLanes + lam] = ch.lane_sum(b, j, lam, false);
 }
@@ -269,8 +296,8 @@ __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
   Chain<DT, LOGITS> ch(a);
   const int b = blockIdx.x;
   const int t = threadIdx.x;
-  int nacc;
-  const int j = ch.decide(b, &nacc);
+  const int j = a.dec[2 * b];  // the residual kernel's decision
+  const int nacc = a.dec[2 * b + 1];
   const int64_t G = ceil_div(a.V, kGroup);
 
   for (int l = t; l < kLanes; l += 256) tree[l] = a.lanes[(int64_t)b * kLanes + l];
@@ -839,17 +866,18 @@ extern "C" int bsx_accept_greedy_noalloc(const int64_t* draft_d, const int64_t* 
 }
 
 static int64_t chain_ws_layout(int B, int k, int64_t V, bool logits, int64_t* off_lanes,
-                               int64_t* off_gsum) {
+                               int64_t* off_gsum, int64_t* off_dec) {
   const int64_t rows = (int64_t)B * (2 * k + 1);
   const int64_t stats = logits ? acc::align256(rows * 8) : 0;
   *off_lanes = stats;
   *off_gsum = stats + acc::align256((int64_t)B * canon::kLanes * 4);
-  return *off_gsum + acc::align256((int64_t)B * ceil_div(V, canon::kGroup) * 4);
+  *off_dec = *off_gsum + acc::align256((int64_t)B * ceil_div(V, canon::kGroup) * 4);
+  return *off_dec + acc::align256((int64_t)B * 8);
 }
 
 extern "C" int64_t bsx_chain_ws_bytes(int B, int k, int64_t vocab) {
-  int64_t a, b;
-  return chain_ws_layout(B, k, vocab, true, &a, &b);
+  int64_t a, b, c;
+  return chain_ws_layout(B, k, vocab, true, &a, &b, &c);
 }
 
 template <int DT, bool LOGITS>
@@ -883,8 +911,8 @@ extern "C" int bsx_chain_speculative_sampling(const float* draft_probs_d,
   int rc = check_chain_common(draft_ids_d, uniforms_d, B, k, vocab, out_ids_d, accepted_d, emitted_d);
   if (rc != BSX_OK || B == 0) return rc;
   BSX_REQUIRE(target_probs_d, BSX_ERR_INVALID, "null target_probs");
-  int64_t off_lanes, off_gsum;
-  const int64_t need = chain_ws_layout(B, k, vocab, false, &off_lanes, &off_gsum);
+  int64_t off_lanes, off_gsum, off_dec;
+  const int64_t need = chain_ws_layout(B, k, vocab, false, &off_lanes, &off_gsum, &off_dec);
   BSX_REQUIRE(ws_d && ws_bytes >= need, BSX_ERR_CAPACITY, "chain workspace too small (%lld < %lld)",
               (long long)ws_bytes, (long long)need);
   acc::ChainArgs a{};
@@ -897,6 +925,7 @@ extern "C" int bsx_chain_speculative_sampling(const float* draft_probs_d,
   a.V = vocab;
   a.lanes = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_lanes);
   a.gsum = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_gsum);
+  a.dec = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) + off_dec);
   a.out_ids = out_ids_d;
   a.accepted = accepted_d;
   a.emitted = emitted_d;
@@ -927,8 +956,8 @@ extern "C" int bsx_chain_speculative_sampling_logits(const void* draft_logits_d,
   BSX_REQUIRE(target_logits_d, BSX_ERR_INVALID, "null target_logits");
   BSX_REQUIRE(temperature > 0.f && temperature == temperature, BSX_ERR_INVALID,
               "temperature must be > 0 (greedy acceptance has its own entry point)");
-  int64_t off_lanes, off_gsum;
-  const int64_t need = chain_ws_layout(B, k, vocab, true, &off_lanes, &off_gsum);
+  int64_t off_lanes, off_gsum, off_dec;
+  const int64_t need = chain_ws_layout(B, k, vocab, true, &off_lanes, &off_gsum, &off_dec);
   BSX_REQUIRE(ws_d && ws_bytes >= need, BSX_ERR_CAPACITY, "chain workspace too small (%lld < %lld)",
               (long long)ws_bytes, (long long)need);
   acc::ChainArgs a{};
@@ -943,6 +972,7 @@ extern "C" int bsx_chain_speculative_sampling_logits(const void* draft_logits_d,
   a.V = vocab;
   a.lanes = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_lanes);
   a.gsum = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_gsum);
+  a.dec = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) + off_dec);
   a.out_ids = out_ids_d;
   a.accepted = accepted_d;
   a.emitted = emitted_d;
