@@ -104,6 +104,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._mask_words: Optional[torch.Tensor] = None
         self._blob_bytes = 0
         self._pinned: Optional[torch.Tensor] = None
+        self._pinned_tab: Optional[torch.Tensor] = None
         self._copy_done: Optional[torch.cuda.Event] = None
         self._dtype: Optional[torch.dtype] = None
         # device plans: the int32 page-table tensors the planner reads (kept alive while
@@ -176,9 +177,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
                                  sink_tokens, window_tokens, max_qo_len, non_blocking)
             return
 
-        qo_h = _host_i32(qo_indptr)
-        kvp_h = _host_i32(paged_kv_indptr)
-        last_h = _host_i32(paged_kv_last_page_len)
+        qo_h, kvp_h, last_h = self._host_tables(qo_indptr, paged_kv_indptr,
+                                                paged_kv_last_page_len)
         batch = int(qo_h.shape[0]) - 1
         if batch < 0 or kvp_h.shape[0] != batch + 1 or last_h.shape[0] < batch:
             raise ValueError("qo_indptr, paged_kv_indptr and paged_kv_last_page_len disagree on batch")
@@ -265,6 +265,31 @@ class BatchPrefillWithPagedKVCacheWrapper:
             self._set_mask_words(words, int(plan.total_qo))
         self._plan = plan
         self._dtype = qdt
+
+    def _host_tables(self, *tables: torch.Tensor) -> list:
+        """Host int32 copies of the page-table arrays the host planner reads.  Device
+        tensors are copied on the current stream into one pinned staging buffer and read
+        after a single synchronisation (a copy per array would synchronise per array)."""
+        if not all(t.is_cuda for t in tables):
+            return [_host_i32(t) for t in tables]
+        sizes = [t.numel() for t in tables]
+        total = sum(sizes)
+        if self._pinned_tab is None or self._pinned_tab.numel() < total:
+            self._pinned_tab = torch.empty(max(total, 4096), dtype=torch.int32, pin_memory=True)
+        with torch.cuda.device(tables[0].device):
+            off = 0
+            for t, n in zip(tables, sizes):
+                src = t.detach().reshape(-1)
+                if src.dtype != torch.int32:
+                    src = src.to(torch.int32)
+                self._pinned_tab[off:off + n].copy_(src, non_blocking=True)
+                off += n
+            torch.cuda.current_stream().synchronize()
+        out, off = [], 0
+        for n in sizes:
+            out.append(self._pinned_tab[off:off + n].numpy().copy())
+            off += n
+        return out
 
     def _fixed_shape(self, lib, batch: int, max_qo: int, static: tuple) -> _lib.AttnPlan:
         """The bound-sized shape of graph mode: kept while plans fit it (same heads, page
