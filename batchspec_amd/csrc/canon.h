@@ -131,15 +131,24 @@ BSX_HD uint32_t okey(float x) {
 BSX_HD float key_value(uint32_t k) {
   return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
-// Fixed-point mass of a weight: trunc(w * 2^40) (w * 2^40 is exact), 0 unless w > 0,
-// read off the bits (finite w below 2^23).
+// Fixed-point mass of a weight: trunc(w * 2^40) (w * 2^40 is exact), 0 unless w > 0
+// (finite w below 2^23).  On the device from a = w * 2^8 with two conversions: the
+// integer part floor(a) * 2^32 + trunc(fract(a) * 2^32), both parts exact; on the host
+// read off the bits.
 BSX_HD uint64_t fx40(float w) {
+#ifdef __HIP_DEVICE_COMPILE__
+  const float a = fmaxf(w, 0.0f) * 0x1p8f;  // NaN and w <= 0 give 0
+  const uint32_t hi = (uint32_t)a;
+  const uint32_t lo = (uint32_t)((a - (float)hi) * 0x1p32f);
+  return ((uint64_t)hi << 32) | lo;
+#else
   if (!(w > 0.0f)) return 0ull;
   const uint32_t b = __builtin_bit_cast(uint32_t, w * 0x1p40f);
   const int e = (int)(b >> 23) - 150;  // value = mant * 2^e
   const uint64_t mant = (uint64_t)((b & 0x7fffffu) | 0x800000u);
   if ((b >> 23) == 0u) return 0ull;    // below 1
   return e >= 0 ? mant << e : (e > -24 ? mant >> -e : 0ull);
+#endif
 }
 // Round-to-nearest-even conversion of a 64-bit integer to binary32.
 BSX_HD float u64_to_f32(uint64_t v) {

@@ -39,12 +39,19 @@
 //        gives t* and Z_K exactly, and the kept indices are written out;
 //     3. if the list overflowed (or the row is too short for step 1), the bound of all
 //        2048 lane maxima and a second read of the row list the candidates again;
-//     4. if that fails too (ties, a large k, a nucleus below the bound), an exact radix
-//        select over the key bits, 8 per pass, with counts and fixed-point masses per
-//        digit in LDS; the row then gets no list.
+//     4. if that fails too (a top_k above kCands, a nucleus below the bound), a
+//        histogram of counts and masses over 1024 bins of the weight's exponent picks
+//        the bin that holds t*; its elements (or, for a bin of more than kCands, those
+//        of one of its 1024 sub-bins, after a histogram of them) are listed and walked
+//        with the count and mass above them as the base; the row gets no list;
+//     5. if a sub-bin is still too dense (ties), an exact radix select over the key
+//        bits, 8 per pass, with counts and fixed-point masses per digit in LDS.
+//   filter_tiles_kernel: (request, part) workgroups: the ratio tests, then, when the
+//     row the chain stops at has no kept list, the fixed-point sums of its draw weights
+//     over wave-sized tiles of the row, 16 tiles per workgroup;
 //   filter_chain_kernel: one workgroup per request: the ratio tests, then the draw
-//     from the row the chain stops at, over its kept list, or over the whole row in
-//     wave-sized tiles (tile sums, their prefix, the lane, the element) without one.
+//     from the row the chain stops at, over its kept list, or from the tile sums (their
+//     prefix, the tile, the lane, the element) without one.
 //   filtered_probs_kernel: p'(x) for every element (get_sampling_probs).
 #include <limits.h>
 
@@ -76,6 +83,14 @@ static_assert(kCap <= kThreads, "one kept element per thread in the draw");
 static_assert(kMaxTiles % kThreads == 0, "tiles split evenly over threads");
 static_assert(kCands % kThreads == 0 && kCands * 8 <= kBins * 4, "candidate masses fit hist");
 static_assert(kBins % (4 * kThreads) == 0 && 4 * (kBins / kThreads) <= 64, "bound scan layout");
+// Log2-weight bins of the large-threshold select: kYScale bins per unit of the weight's
+// exponent y, the last bin from y <= -(kYBins - 1) / kYScale < -40.9 on, where every
+// fixed-point mass is 0.
+constexpr int kYBins = 1024;
+constexpr float kYScale = 25.0f;
+static_assert(kYBins * 8 <= kBins * 4 && kYBins <= kCands && kYBins % kThreads == 0,
+              "bin masses fit hist, bin counts fit ckey / cidx");
+static_assert((kYBins - 1) / kYScale > 40.5f, "the last bin holds mass 0 only");
 
 struct RowInfo {
   float m;        // row max M
@@ -350,12 +365,14 @@ struct Collector {
 };
 
 // Threshold from a complete list of the candidates [0, n) (every element of the row
-// at or above the smallest listed key is listed): each candidate gets the count and
-// mass of the listed keys at or above its own; t* is the largest key that reaches the
-// target.  Writes the kept indices (at most kCap, else the row gets no list).
-// Returns false (in every thread) when no listed key reaches the target.
+// at or above the smallest listed key and below the keys counted in base_c / base_m
+// is listed): each candidate gets base_c / base_m plus the count and mass of the listed
+// keys at or above its own; t* is the largest key that reaches the target.  Writes the
+// kept indices (at most kCap, else the row gets no list; no list either when list_out
+// is null).  Returns false (in every thread) when no listed key reaches the target.
 __device__ bool walk(RowsLds& L, int n, float c, float neg, bool use_k, bool use_p, int top_k,
-                     uint64_t target, int32_t* list_out) {
+                     uint64_t target, int32_t* list_out, uint32_t base_c = 0u,
+                     uint64_t base_m = 0ull) {
   typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
   const int t = threadIdx.x;
   uint64_t* cm = reinterpret_cast<uint64_t*>(L.hist);
@@ -382,7 +399,7 @@ __device__ bool walk(RowsLds& L, int n, float c, float neg, bool use_k, bool use
     __syncthreads();
     if (mine != 0ull) atomicAdd(reinterpret_cast<unsigned long long*>(&L.zk), (unsigned long long)mine);
     __syncthreads();
-    const bool enough = L.zk >= target;
+    const bool enough = base_m + L.zk >= target;
     __syncthreads();
     if (!enough) return false;
   }
@@ -393,8 +410,8 @@ __device__ bool walk(RowsLds& L, int n, float c, float neg, bool use_k, bool use
   for (int j = 0; j < PER; ++j) {
     const int s = t + kThreads * j;
     key[j] = s < n ? L.ckey[s] : 0xffffffffu;
-    cnt[j] = 0u;
-    mass[j] = 0ull;
+    cnt[j] = base_c;
+    mass[j] = base_m;
   }
   if (n <= kThreads) {
     // one candidate per thread; every listed key against it, 8 at a time from 16-byte
@@ -440,16 +457,216 @@ __device__ bool walk(RowsLds& L, int n, float c, float neg, bool use_k, bool use
     const int s = t + kThreads * j;
     if (s < n) {
       if (key[j] == tk) L.zk = mass[j];  // equal keys hold equal masses
-      if (key[j] >= tk) {
+      if (list_out != nullptr && key[j] >= tk) {
         const int slot = atomicAdd(&L.nk, 1);
         if (slot < kCap) list_out[slot] = L.cidx[s];
       }
     }
   }
   __syncthreads();
-  if (t == 0 && L.nk > kCap) L.nk = -1;
+  if (t == 0 && (list_out == nullptr || L.nk > kCap)) L.nk = -1;
   __syncthreads();
   return true;
+}
+
+// Position of an element on the log2-weight axis: q = -y * kYScale with
+// y = fma(x, C, -(M C)), the exponent of its weight.  Its bin is floor(q) below
+// kYBins - 1 and the last bin otherwise (NaN included); the sub-bins of bin b split
+// [b, b + 1) into kYBins.  A larger key never gets a larger q, bin or sub-bin, so every
+// bin (sub-bin) holds a contiguous range of keys.
+__device__ __forceinline__ float ypos(float x, float c, float neg) {
+  return -fmaf(x, c, neg) * kYScale;
+}
+__device__ __forceinline__ int ybin(float q) {
+  return q < (float)(kYBins - 1) ? (int)fmaxf(q, 0.0f) : kYBins - 1;
+}
+// q - b is exact for q in [b, b + 1) (b >= 1), and q itself for b = 0.
+__device__ __forceinline__ int ysub(float q, int b) {
+  return min((int)fmaxf((q - (float)b) * (float)kYBins, 0.0f), kYBins - 1);
+}
+
+// The first of the bins [0, nb) (in decreasing key order) at which base + the running
+// count / mass of cnt / mass reaches the threshold.  Returns it (-1 if none does) and
+// leaves what lies above it in L.above_c / L.above_m and its own count in L.rcount.
+// Uses part.  Every thread calls it.
+__device__ int ybin_first(RowsLds& L, const uint32_t* cnt, const uint64_t* mass, int nb,
+                          uint32_t base_c, uint64_t base_m, bool use_k, bool use_p, int top_k,
+                          uint64_t target) {
+  constexpr int PER = kYBins / kThreads;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  uint32_t cc[PER];
+  uint64_t mm[PER];
+  uint64_t sc = 0ull, sm = 0ull;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    cc[i] = cnt[PER * t + i];
+    mm[i] = mass[PER * t + i];
+    sc += cc[i];
+    sm += mm[i];
+  }
+  const uint64_t ic = wave_prefix_u64(sc), im = wave_prefix_u64(sm);
+  uint64_t* wt = reinterpret_cast<uint64_t*>(L.part);  // wave totals: counts, then masses
+  if (lane == 63) {
+    wt[wave] = ic;
+    wt[kThreads / 64 + wave] = im;
+  }
+  if (t == 0) L.bin = INT_MAX;
+  __syncthreads();
+  uint64_t ac = base_c + (ic - sc), am = base_m + (im - sm);
+  for (int w = 0; w < wave; ++w) {
+    ac += wt[w];
+    am += wt[kThreads / 64 + w];
+  }
+  int mine = -1;
+  uint32_t my_c = 0u, my_n = 0u;
+  uint64_t my_m = 0ull;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int b = PER * t + i;
+    if (mine < 0 && b < nb &&
+        reached(use_k, use_p, (uint32_t)(ac + cc[i]), am + mm[i], top_k, target)) {
+      mine = b;
+      my_c = (uint32_t)ac;
+      my_m = am;
+      my_n = cc[i];
+    }
+    ac += cc[i];
+    am += mm[i];
+  }
+  if (mine >= 0) atomicMin(&L.bin, mine);
+  __syncthreads();
+  const int first = L.bin;
+  if (mine >= 0 && mine == first) {
+    L.above_c = my_c;
+    L.above_m = my_m;
+    L.rcount = (int)my_n;
+  }
+  __syncthreads();
+  return first == INT_MAX ? -1 : first;
+}
+
+// Counts (in ckey) and, with MASS, masses (in hist; else 0) of the elements per bin
+// (b0 < 0) or per sub-bin of bin b0, the last bin left out.
+template <int DT, bool MASS>
+__device__ void ybin_hist(RowsLds& L, const void* row, int64_t V, bool vec, float c, float neg,
+                          int b0) {
+  uint32_t* cnt = L.ckey;
+  uint64_t* mass = reinterpret_cast<uint64_t*>(L.hist);
+  for (int i = threadIdx.x; i < kYBins; i += kThreads) {
+    cnt[i] = 0u;
+    mass[i] = 0ull;
+  }
+  __syncthreads();
+  for_each_element<DT>(row, V, vec, [&](float x, int64_t) {
+    const float q = ypos(x, c, neg);
+    int b = ybin(q);
+    if (b == kYBins - 1 || (b0 >= 0 && b != b0)) return;
+    if (b0 >= 0) b = ysub(q, b0);
+    atomicAdd(&cnt[b], 1u);
+    if constexpr (MASS) {
+      const uint64_t m = fx40(canon::weight(x, c, neg));
+      if (m != 0ull)
+        atomicAdd(reinterpret_cast<unsigned long long*>(&mass[b]), (unsigned long long)m);
+    }
+  });
+  __syncthreads();
+}
+
+// Threshold of a row whose upper set is too large to list: the first log2-weight bin
+// (one histogram pass) at which the running count / mass reaches the target, a
+// histogram of its sub-bins when it holds more than kCands elements (a second pass),
+// then the elements of that bin (sub-bin) listed and walked with what lies above as the
+// base; a listed bin with more than kThreads elements is narrowed to one of its
+// sub-bins first (in LDS).  For top-k alone the histograms count only, and the listing
+// pass sums the masses above.  The row gets no list.  Returns false (in every thread)
+// when the threshold is not found this way (a bin too dense, or a target beyond the
+// mass of the bins).  Needs a finite row max.
+template <int DT>
+__device__ bool ybin_threshold(RowsLds& L, const void* row, int64_t V, bool vec, float c,
+                               float neg, bool use_k, bool use_p, int top_k, uint64_t target) {
+  const int t = threadIdx.x;
+  if (use_p) ybin_hist<DT, true>(L, row, V, vec, c, neg, -1);
+  else ybin_hist<DT, false>(L, row, V, vec, c, neg, -1);
+  const int b0 = ybin_first(L, L.ckey, reinterpret_cast<const uint64_t*>(L.hist), kYBins - 1,
+                            0u, 0ull, use_k, use_p, top_k, target);
+  if (b0 < 0) return false;
+  uint32_t base_c = L.above_c;
+  uint64_t base_m = L.above_m;
+  int b1 = -1;
+  if (L.rcount > kCands) {
+    if (use_p) ybin_hist<DT, true>(L, row, V, vec, c, neg, b0);
+    else ybin_hist<DT, false>(L, row, V, vec, c, neg, b0);
+    b1 = ybin_first(L, L.ckey, reinterpret_cast<const uint64_t*>(L.hist), kYBins, base_c, base_m,
+                    use_k, use_p, top_k, target);
+    if (b1 < 0 || L.rcount > kCands) return false;
+    base_c = L.above_c;
+    base_m = L.above_m;
+  }
+  if (t == 0) {
+    L.count = 0;
+    L.zk = 0ull;
+  }
+  __syncthreads();
+  uint64_t above = 0ull;  // top-k alone: the mass of the elements above the listed ones
+  for_each_element<DT>(row, V, vec, [&](float x, int64_t) {
+    const float q = ypos(x, c, neg);
+    const int b = ybin(q);
+    const int sb = b1 >= 0 && b == b0 ? ysub(q, b0) : -1;
+    if (b == b0 && sb == b1) {
+      const int slot = atomicAdd(&L.count, 1);
+      if (slot < kCands) L.ckey[slot] = okey(x);
+    } else if (!use_p && (b < b0 || (b == b0 && sb < b1))) {
+      above += fx40(canon::weight(x, c, neg));
+    }
+  });
+  if (!use_p) {
+    above = wave_sum_u64(above);
+    if ((t & 63) == 0 && above != 0ull)
+      atomicAdd(reinterpret_cast<unsigned long long*>(&L.zk), (unsigned long long)above);
+  }
+  __syncthreads();
+  if (!use_p) base_m = L.zk;
+  int n = L.count;
+  if (n > kCands) return false;
+  if (n > kThreads && b1 < 0) {
+    // sub-bins of the listed elements: counts in cidx, masses in hist
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(L.cidx);
+    uint64_t* mass = reinterpret_cast<uint64_t*>(L.hist);
+    for (int i = t; i < kYBins; i += kThreads) {
+      cnt[i] = 0u;
+      mass[i] = 0ull;
+    }
+    __syncthreads();
+    for (int s = t; s < n; s += kThreads) {
+      const float x = key_value(L.ckey[s]);
+      const int sb = ysub(ypos(x, c, neg), b0);
+      atomicAdd(&cnt[sb], 1u);
+      const uint64_t m = fx40(canon::weight(x, c, neg));
+      if (m != 0ull) atomicAdd(reinterpret_cast<unsigned long long*>(&mass[sb]), (unsigned long long)m);
+    }
+    __syncthreads();
+    const int s1 = ybin_first(L, cnt, mass, kYBins, base_c, base_m, use_k, use_p, top_k, target);
+    if (s1 < 0) return false;
+    base_c = L.above_c;
+    base_m = L.above_m;
+    // keep the elements of sub-bin s1, in place
+    constexpr int PER = kCands / kThreads;
+    uint32_t kk[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int s = t + kThreads * j;
+      kk[j] = s < n ? L.ckey[s] : 0u;
+    }
+    if (t == 0) L.count = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (t + kThreads * j < n && ysub(ypos(key_value(kk[j]), c, neg), b0) == s1)
+        L.ckey[atomicAdd(&L.count, 1)] = kk[j];
+    __syncthreads();
+    n = L.count;
+  }
+  return walk(L, n, c, neg, use_k, use_p, top_k, target, nullptr, base_c, base_m);
 }
 
 template <int DT>
@@ -475,7 +692,7 @@ __global__ void __launch_bounds__(kThreads) filter_rows_kernel(RowsArgs a) {
   // (the bound comes from it) and the hit masks cover the whole rounds.
   const int64_t G_whole = V / kGroup;
   Collector<DT> col{&L, INFINITY,
-                    vec && k_eff <= 2048 && ceil_div(G_whole, (int64_t)kThreads * 8) <= kMaxHitRounds,
+                    vec && k_eff <= kCands && ceil_div(G_whole, (int64_t)kThreads * 8) <= kMaxHitRounds,
                     k_eff, {0ull, 0ull}};
   float lm[8];
   acc::row_stats<DT, true, Collector<DT>>(row, V, vec, c, &L.m, &L.z, lm, &col);
@@ -553,8 +770,9 @@ __global__ void __launch_bounds__(kThreads) filter_rows_kernel(RowsArgs a) {
   const bool early = col.on && L.count <= kCands;
   if (early) listed = walk(L, L.count, c, neg, use_k, use_p, a.top_k, target, list_out);
 
-  // 2. otherwise the bound of all lane maxima, and a second read of the row
-  if (!listed && !early) {
+  // 2. otherwise the bound of all lane maxima, and a second read of the row (a list
+  //    cannot hold more than kCands of the top-k)
+  if (!listed && !early && k_eff <= kCands) {
     const uint32_t kb = kth_key(L, lm, k_eff);
     const bool all = kb == 0u;
     if (!all || V <= kCands) {
@@ -568,7 +786,11 @@ __global__ void __launch_bounds__(kThreads) filter_rows_kernel(RowsArgs a) {
     }
   }
 
-  // 3. exact radix select
+  // 3. log2-weight bins
+  if (!listed && neg > -INFINITY && neg < INFINITY)
+    listed = ybin_threshold<DT>(L, row, V, vec, c, neg, use_k, use_p, a.top_k, target);
+
+  // 4. exact radix select
   if (!listed) {
     uint32_t* hc = L.hist;                                     // [256]
     uint64_t* hm = reinterpret_cast<uint64_t*>(L.hist + 256);  // [256]
@@ -654,10 +876,22 @@ struct ChainArgs {
   int B, k;
   int64_t V;
   float c;
+  uint64_t* tiles;   // [B][2][draw_tiles(V)] tile sums of the whole-row draws
   int32_t* out_ids;  // [B, k+1]
   int32_t* accepted;
   int32_t* emitted;
 };
+
+// Tiles of a whole-row draw: 64 lanes x E consecutive elements (E a multiple of 8), at
+// most kMaxTiles of them; filter_tiles_kernel sums kTilesPerPart per workgroup.
+constexpr int kTilesPerPart = 16;
+static_assert(kTilesPerPart % (kThreads / 64) == 0, "whole tiles per wave");
+__host__ __device__ inline int draw_tile_elems(int64_t V) {
+  return kGroup * (int)ceil_div(V, (int64_t)kMaxTiles * 64 * kGroup);
+}
+__host__ __device__ inline int draw_tiles(int64_t V) {
+  return (int)ceil_div(V, 64LL * draw_tile_elems(V));
+}
 
 template <int DT>
 struct Filtered {
@@ -699,6 +933,155 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* s_acc) {
   return total;
 }
 
+// Ratio tests of request b, by the first wave (lane i tests draft position i): the
+// first rejected position (k if none) in *s_j, the number accepted in *s_n.
+template <int DT>
+__device__ void ratio_tests(const ChainArgs& a, int b, int* s_j, int* s_n) {
+  const int t = threadIdx.x;
+  if (t >= 64) return;
+  const int k = a.k;
+  const int64_t V = a.V;
+  const int64_t trow0 = (int64_t)b * (k + 1);
+  const int64_t drow0 = (int64_t)a.B * (k + 1) + (int64_t)b * k;
+  int j = k, cnt = 0;
+  for (int i0 = 0; i0 < k; i0 += 64) {
+    const int i = i0 + t;
+    bool acc = false;
+    if (i < k) {
+      const int64_t x = a.draft_ids[(int64_t)b * k + i];
+      if (x >= 0 && x < V) {
+        const float p = filtered_row<DT>(a.t_logits, trow0 + i, V, a.info[trow0 + i], a.c).p(x);
+        const float q = a.d_logits
+                            ? filtered_row<DT>(a.d_logits, (int64_t)b * k + i, V,
+                                               a.info[drow0 + i], a.c).p(x)
+                            : 1.0f;
+        acc = a.uniforms[trow0 + i] * q < p;
+      }
+    }
+    const uint64_t acc_bits = __builtin_amdgcn_ballot_w64(acc);
+    const uint64_t rej_bits = __builtin_amdgcn_ballot_w64(i < k && !acc);
+    cnt += __builtin_popcountll(acc_bits);
+    if (j == k && rej_bits != 0) j = i0 + __builtin_ctzll(rej_bits);
+  }
+  if (t == 0) {
+    *s_j = j;
+    *s_n = cnt;
+  }
+}
+
+// Fixed-point weights of the draw of a request whose chain stops at position j:
+// r(v) = fx40(max(p'(v) - q'(v), 0)) against the draft (its filtered probability, or one
+// at the draft token for a one-hot draft) when j < k, and fx40(p'(v)) without it (all
+// accepted, or a residual that sums to 0).
+template <int DT>
+struct DrawRow {
+  Filtered<DT> P, Q;
+  bool has_q, qlog, vec8;
+  int64_t xj, V;
+
+  __device__ uint64_t at(int64_t v, bool with_q) const {
+    const float p = P.p(v);
+    if (!with_q) return fx40(p);
+    const float q = qlog ? Q.p(v) : (v == xj ? 1.0f : 0.0f);
+    return fx40(fmaxf(p - q, 0.0f));
+  }
+  // both weights of the 8 elements [v0, v0 + 8) (v0 a multiple of 8): rq against the
+  // draft (when has_q), rp without; one 16-byte load per row when the rows allow it
+  __device__ void at8(int64_t v0, uint64_t (&rq)[8], uint64_t (&rp)[8]) const {
+    if (vec8 && v0 + 8 <= V) {
+      float p[8], q[8];
+      P.p8(v0, p);
+      if (has_q && qlog) Q.p8(v0, q);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        rp[e] = fx40(p[e]);
+        if (has_q) {
+          const float qe = qlog ? q[e] : (v0 + e == xj ? 1.0f : 0.0f);
+          rq[e] = fx40(fmaxf(p[e] - qe, 0.0f));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        rp[e] = v0 + e < V ? at(v0 + e, false) : 0ull;
+        if (has_q) rq[e] = v0 + e < V ? at(v0 + e, true) : 0ull;
+      }
+    }
+  }
+  // sums of rq and rp over the E elements [v0, v0 + E) (E a multiple of 8)
+  __device__ void sums(int64_t v0, int E, uint64_t& sq, uint64_t& sp) const {
+    sq = 0ull;
+    sp = 0ull;
+    for (int e0 = 0; e0 < E && v0 + e0 < V; e0 += 8) {
+      uint64_t rq[8], rp[8];
+      at8(v0 + e0, rq, rp);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sp += rp[e];
+        if (has_q) sq += rq[e];
+      }
+    }
+  }
+};
+
+template <int DT>
+__device__ DrawRow<DT> draw_row(const ChainArgs& a, int b, int j) {
+  const int k = a.k;
+  const int64_t V = a.V;
+  const int64_t trow = (int64_t)b * (k + 1) + j;
+  DrawRow<DT> d;
+  d.V = V;
+  d.P = filtered_row<DT>(a.t_logits, trow, V, a.info[trow], a.c);
+  d.has_q = j < k;
+  d.qlog = d.has_q && a.d_logits != nullptr;
+  d.xj = d.has_q ? a.draft_ids[(int64_t)b * k + j] : -1;
+  d.Q = Filtered<DT>{};
+  if (d.qlog)
+    d.Q = filtered_row<DT>(a.d_logits, (int64_t)b * k + j, V,
+                           a.info[(int64_t)a.B * (k + 1) + (int64_t)b * k + j], a.c);
+  const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
+  d.vec8 = (V * (int64_t)esz) % 16 == 0 && ((uintptr_t)d.P.row) % 16 == 0 &&
+           (!d.qlog || ((uintptr_t)d.Q.row) % 16 == 0);
+  return d;
+}
+
+// Tile sums of a whole-row draw: grid (B, parts); part p sums the tiles
+// [kTilesPerPart p, kTilesPerPart (p + 1)) of the row request b's chain stops at, one
+// wave per tile, into tiles[b][0][T] (against the draft) and tiles[b][1][T] (without),
+// unless that row has a kept list.
+template <int DT>
+__global__ void __launch_bounds__(kThreads) filter_tiles_kernel(ChainArgs a) {
+  __shared__ int s_j, s_n;
+  const int b = blockIdx.x;
+  ratio_tests<DT>(a, b, &s_j, &s_n);
+  __syncthreads();
+  const int j = s_j;
+  if (a.info[(int64_t)b * (a.k + 1) + j].n_list >= 0) return;
+  const DrawRow<DT> R = draw_row<DT>(a, b, j);
+  const int E = draw_tile_elems(a.V);
+  const int ntiles = draw_tiles(a.V);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint64_t* ts = a.tiles + (int64_t)b * 2 * ntiles;
+  constexpr int U = kTilesPerPart / (kThreads / 64);
+  uint64_t sq[U], sp[U];
+  // the tiles of a wave summed together: their loads go out together
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int T = blockIdx.y * kTilesPerPart + (kThreads / 64) * u + wave;
+    R.sums((int64_t)(T < ntiles ? T : 0) * 64 * E + (int64_t)lane * E, E, sq[u], sp[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int T = blockIdx.y * kTilesPerPart + (kThreads / 64) * u + wave;
+    const uint64_t q = R.has_q ? wave_sum_u64(sq[u]) : 0ull;
+    const uint64_t p = wave_sum_u64(sp[u]);
+    if (lane == 0 && T < ntiles) {
+      ts[T] = q;
+      ts[ntiles + T] = p;
+    }
+  }
+}
+
 template <int DT>
 __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
   __shared__ int s_j, s_n, s_tok, s_last, s_tile, s_last_tile;
@@ -712,76 +1095,18 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
   const int k = a.k;
   const int64_t V = a.V;
   const int64_t trow0 = (int64_t)b * (k + 1);
-  const int64_t drow0 = (int64_t)a.B * (k + 1) + (int64_t)b * k;
 
-  // ratio tests: lane i of the first wave tests draft position i
-  if (t < 64) {
-    int j = k, cnt = 0;
-    for (int i0 = 0; i0 < k; i0 += 64) {
-      const int i = i0 + t;
-      bool acc = false;
-      if (i < k) {
-        const int64_t x = a.draft_ids[(int64_t)b * k + i];
-        if (x >= 0 && x < V) {
-          const float p = filtered_row<DT>(a.t_logits, trow0 + i, V, a.info[trow0 + i], a.c).p(x);
-          const float q = a.d_logits
-                              ? filtered_row<DT>(a.d_logits, (int64_t)b * k + i, V,
-                                                 a.info[drow0 + i], a.c).p(x)
-                              : 1.0f;
-          acc = a.uniforms[trow0 + i] * q < p;
-        }
-      }
-      const uint64_t acc_bits = __builtin_amdgcn_ballot_w64(acc);
-      const uint64_t rej_bits = __builtin_amdgcn_ballot_w64(i < k && !acc);
-      cnt += __builtin_popcountll(acc_bits);
-      if (j == k && rej_bits != 0) j = i0 + __builtin_ctzll(rej_bits);
-    }
-    if (t == 0) {
-      s_j = j;
-      s_n = cnt;
-      s_tok = INT_MAX;
-      s_last = -1;
-      s_last_tile = 0;
-    }
+  ratio_tests<DT>(a, b, &s_j, &s_n);
+  if (t == 0) {
+    s_tok = INT_MAX;
+    s_last = -1;
+    s_last_tile = 0;
   }
   __syncthreads();
   const int j = s_j;
   const RowInfo ti = a.info[trow0 + j];
-  const Filtered<DT> P = filtered_row<DT>(a.t_logits, trow0 + j, V, ti, a.c);
-  const bool has_q = j < k;
-  const int64_t xj = has_q ? a.draft_ids[(int64_t)b * k + j] : -1;
-  Filtered<DT> Q{};
-  if (has_q && a.d_logits) Q = filtered_row<DT>(a.d_logits, (int64_t)b * k + j, V, a.info[drow0 + j], a.c);
-  auto r_at = [&](int64_t v, bool with_q) -> uint64_t {
-    const float p = P.p(v);
-    if (!with_q) return fx40(p);
-    const float q = a.d_logits ? Q.p(v) : (v == xj ? 1.0f : 0.0f);
-    return fx40(fmaxf(p - q, 0.0f));
-  };
-  // r_at of the 8 elements [v0, v0 + 8) (v0 a multiple of 8): one 16-byte load per row
-  // when the rows allow it
-  const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
-  const bool vec8 = (V * (int64_t)esz) % 16 == 0 && ((uintptr_t)P.row) % 16 == 0 &&
-                    (!(has_q && a.d_logits) || ((uintptr_t)Q.row) % 16 == 0);
-  auto r8 = [&](int64_t v0, bool with_q, uint64_t (&r)[8]) {
-    if (vec8 && v0 + 8 <= V) {
-      float p[8], q[8];
-      P.p8(v0, p);
-      if (with_q && a.d_logits) Q.p8(v0, q);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (!with_q) {
-          r[e] = fx40(p[e]);
-        } else {
-          const float qe = a.d_logits ? q[e] : (v0 + e == xj ? 1.0f : 0.0f);
-          r[e] = fx40(fmaxf(p[e] - qe, 0.0f));
-        }
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) r[e] = v0 + e < V ? r_at(v0 + e, with_q) : 0ull;
-    }
-  };
+  const DrawRow<DT> R = draw_row<DT>(a, b, j);
+  const bool has_q = R.has_q;
   const float u = a.uniforms[trow0 + k];
   int tok = -1;
   if (ti.n_list >= 0) {
@@ -791,7 +1116,7 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
     for (int pass = 0; pass < 2; ++pass) {
       const bool with_q = has_q && pass == 0;
       if (pass == 1 && !has_q) break;
-      const uint64_t w = t < n ? r_at(v, with_q) : 0ull;
+      const uint64_t w = t < n ? R.at(v, with_q) : 0ull;
       if (t < n) {
         lv[t] = v;
         lr[t] = w;
@@ -812,45 +1137,20 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
       tok = s_tok != INT_MAX ? s_tok : s_last;
     }
   } else {
-    // No list: the whole row, in tiles of 64 lanes x E consecutive elements (one wave
-    // per tile, at most kMaxTiles tiles): tile sums, their prefix, then the lane and
-    // the element inside the tile that holds the draw point.
-    const int E = kGroup * (int)ceil_div(V, (int64_t)kMaxTiles * 64 * kGroup);
+    // No list: the tile sums of filter_tiles_kernel (tiles of 64 lanes x E consecutive
+    // elements), their prefix, then the lane and the element inside the tile that holds
+    // the draw point.
+    const int E = draw_tile_elems(V);
     const int64_t tile = 64LL * E;
-    const int ntiles = (int)ceil_div(V, tile);
+    const int ntiles = draw_tiles(V);
+    const uint64_t* ts = a.tiles + (int64_t)b * 2 * ntiles;
     const int wave = t >> 6, lane = t & 63;
-    auto lane_sum = [&](int T, bool with_q) -> uint64_t {
-      const int64_t v0 = T * tile + (int64_t)lane * E;
-      uint64_t s = 0ull;
-      for (int e0 = 0; e0 < E && v0 + e0 < V; e0 += 8) {
-        uint64_t r[8];
-        r8(v0 + e0, with_q, r);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s += r[e];
-      }
-      return s;
-    };
     uint64_t total = 0ull;
     bool with_q = has_q;
     for (int pass = 0; pass < 2; ++pass) {
       with_q = has_q && pass == 0;
       if (pass == 1 && !has_q) break;
-      // U tiles per wave at a time: their loads go out together
-      constexpr int U = 8;
-      for (int T0 = wave; T0 < ntiles; T0 += (kThreads / 64) * U) {
-        uint64_t ls[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int T = T0 + (kThreads / 64) * u;
-          ls[u] = lane_sum(T < ntiles ? T : T0, with_q);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int T = T0 + (kThreads / 64) * u;
-          const uint64_t s = wave_sum_u64(ls[u]);
-          if (lane == 0 && T < ntiles) tsum[T] = s;
-        }
-      }
+      for (int T = t; T < ntiles; T += kThreads) tsum[T] = ts[(with_q ? 0 : ntiles) + T];
       __syncthreads();
       // thread t: tiles [8t, 8t + 8); exclusive prefix of those groups
       uint64_t mine = 0ull;
@@ -897,21 +1197,23 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
       const bool found = s_tile >= 0;
       const int T = found ? s_tile : s_last_tile;
       if (wave == 0) {
-        const uint64_t ls = lane_sum(T, with_q);
+        const int64_t v0 = T * tile + (int64_t)lane * E;
+        uint64_t sq, sp;
+        R.sums(v0, E, sq, sp);
+        const uint64_t ls = with_q ? sq : sp;
         const uint64_t incl = wave_prefix_u64(ls);
         const uint64_t lexcl = incl - ls;
         if (found) {
           const uint64_t tt = tp - s_tbase;
           if (ls != 0ull && tt >= lexcl && tt < incl) {
             uint64_t cum = lexcl;
-            const int64_t v0 = T * tile + (int64_t)lane * E;
             bool done = false;
             for (int e0 = 0; e0 < E && v0 + e0 < V && !done; e0 += 8) {
-              uint64_t r[8];
-              r8(v0 + e0, with_q, r);
+              uint64_t rq[8], rp[8];
+              R.at8(v0 + e0, rq, rp);
 #pragma unroll
               for (int e = 0; e < 8; ++e) {
-                cum += r[e];
+                cum += with_q ? rq[e] : rp[e];
                 if (!done && cum > tt) {
                   s_tok = (int)(v0 + e0 + e);
                   done = true;
@@ -922,9 +1224,8 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
         } else {
           const uint64_t nz = __builtin_amdgcn_ballot_w64(ls != 0ull);
           if (nz != 0ull && lane == 63 - __builtin_clzll(nz)) {
-            const int64_t v0 = T * tile + (int64_t)lane * E;
             for (int e = E - 1; e >= 0; --e)
-              if (v0 + e < V && r_at(v0 + e, with_q) != 0ull) {
+              if (v0 + e < V && R.at(v0 + e, with_q) != 0ull) {
                 s_tok = (int)(v0 + e);
                 break;
               }
@@ -1005,14 +1306,24 @@ static int filtered_chain_impl(filt::ChainArgs& ca, void* ws, hipStream_t st, in
   int rc = launch_filter_rows<DT>(ca.t_logits, n_t, ca.d_logits, n_d, ca.V, ca.c, top_k, top_p,
                                   ws, st);
   if (rc != BSX_OK) return rc;
+  const int parts = (int)ceil_div(filt::draw_tiles(ca.V), filt::kTilesPerPart);
+  hipLaunchKernelGGL((filt::filter_tiles_kernel<DT>), dim3((unsigned)ca.B, (unsigned)parts),
+                     dim3(filt::kThreads), 0, st, ca);
+  BSX_LAUNCH_CHECK();
   hipLaunchKernelGGL((filt::filter_chain_kernel<DT>), dim3((unsigned)ca.B), dim3(filt::kThreads),
                      0, st, ca);
   BSX_LAUNCH_CHECK();
   return BSX_OK;
 }
 
+// Row infos and lists of the filtered rows, then the tile sums of the whole-row draws.
+static int64_t filtered_chain_tiles_bytes(int B, int64_t vocab) {
+  return filt::align256((int64_t)B * 2 * filt::draw_tiles(vocab) * 8);
+}
+
 extern "C" int64_t bsx_chain_filtered_ws_bytes(int B, int k, int64_t vocab) {
-  const int64_t f = bsx_filter_ws_bytes((int64_t)B * (2 * k + 1));
+  const int64_t f = bsx_filter_ws_bytes((int64_t)B * (2 * k + 1)) +
+                    filtered_chain_tiles_bytes(B, vocab);
   const int64_t u = bsx_chain_ws_bytes(B, k, vocab);
   return f > u ? f : u;
 }
@@ -1036,7 +1347,8 @@ extern "C" int bsx_chain_speculative_sampling_filtered(
               BSX_ERR_INVALID, "null pointer");
   BSX_REQUIRE(temperature > 0.f && temperature == temperature, BSX_ERR_INVALID,
               "temperature must be > 0 (greedy acceptance has its own entry point)");
-  const int64_t need = bsx_filter_ws_bytes((int64_t)B * (2 * k + 1));
+  const int64_t need = bsx_filter_ws_bytes((int64_t)B * (2 * k + 1)) +
+                       filtered_chain_tiles_bytes(B, vocab);
   BSX_REQUIRE(ws_d && ws_bytes >= need, BSX_ERR_CAPACITY, "filter workspace too small (%lld < %lld)",
               (long long)ws_bytes, (long long)need);
   filt::ChainArgs ca{};
@@ -1046,6 +1358,7 @@ extern "C" int bsx_chain_speculative_sampling_filtered(
   const int64_t rows = (int64_t)B * (k + 1) + (draft_logits_d ? (int64_t)B * k : 0);
   ca.lists = reinterpret_cast<const int32_t*>(static_cast<char*>(ws_d) +
                                               filt::align256(rows * (int64_t)sizeof(filt::RowInfo)));
+  ca.tiles = reinterpret_cast<uint64_t*>(static_cast<char*>(ws_d) + bsx_filter_ws_bytes(rows));
   ca.draft_ids = draft_ids_d;
   ca.uniforms = uniforms_d;
   ca.B = B;

@@ -94,6 +94,61 @@ def test_sampling_probs_bit_exact(dt, V, T, top_k, top_p, q):
 
 
 @pytest.mark.parametrize("dt,V,T,top_k,top_p", [
+    ("bf16", 128256, 1.0, 0, 0.95),     # wide nucleus: about a third of the row
+    ("bf16", 128256, 1.0, 0, 0.5),
+    ("bf16", 128256, 1.0, 2000, 0.9),   # top_k above the list capacity
+    ("fp16", 128256, 0.7, 5000, 0.0),
+    ("fp32", 50000, 1.5, 0, 0.99),
+    ("bf16", 40000, 0.3, 0, 0.999),     # low temperature: thresholds far down the exponent axis
+])
+def test_sampling_probs_large_thresholds(dt, V, T, top_k, top_p):
+    """Upper sets too large to list: the threshold comes from the exponent-bin
+    histogram and a walk of one bin."""
+    say(f"get_sampling_probs, large threshold: {dt} V={V} T={T} top_k={top_k} top_p={top_p}")
+    g = torch.Generator().manual_seed(V + top_k)
+    x = (torch.randn((3, V), generator=g) * 2).to(DT[dt])
+    got = S.get_sampling_probs(x.to(DEV), top_p=top_p, top_k=top_k, temperature=T)
+    ref = OAc.filtered_probs(x.float().numpy(), T, top_k, top_p)
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(ref.shape).view(np.int32),
+                                  ref.view(np.int32))
+
+
+def _band_rows(rows, V, n_band, lo, width, seed):
+    """fp32 N(0, 2) rows with n_band elements of each replaced by values spread over
+    [lo, lo + width): many elements inside one bin of the weight's exponent."""
+    g = np.random.default_rng(seed)
+    x = (g.standard_normal((rows, V)) * 2).astype(np.float32)
+    for r in range(rows):
+        idx = g.choice(V, n_band, replace=False)
+        x[r, idx] = (lo + width * g.random(n_band)).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("n_band,by", [(20000, "top_k"), (20000, "top_p"), (600, "top_k"),
+                                       (600, "top_p"), (3000, "top_p")])
+def test_sampling_probs_dense_bin(n_band, by):
+    """The threshold inside a narrow band of many values: a bin of more than 1024
+    elements (a second histogram over its sub-bins) or of a few hundred (narrowed in
+    LDS).  The cut is placed in the middle of the band."""
+    say(f"get_sampling_probs, dense bin: band of {n_band}, cut by {by}")
+    V, lo, width, T = 60000, 2.0, 0.01, 1.0
+    x = _band_rows(2, V, n_band, lo, width, seed=n_band)
+    mid = lo + width / 2
+    if by == "top_k":
+        top_k, top_p = int((x[0] >= mid).sum()), 0.0
+    else:
+        w = np.exp((x[0].astype(np.float64) - x[0].max()) / T)
+        top_k, top_p = 0, float(w[x[0] >= mid].sum() / w.sum())
+    got = S.get_sampling_probs(torch.from_numpy(x).to(DEV), top_p=top_p, top_k=top_k,
+                               temperature=T)
+    ref = OAc.filtered_probs(x, T, top_k, top_p)
+    kept = (ref[0] > 0).sum()
+    assert abs(int(kept) - int((x[0] >= mid).sum())) < n_band // 4  # the cut is in the band
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(ref.shape).view(np.int32),
+                                  ref.view(np.int32))
+
+
+@pytest.mark.parametrize("dt,V,T,top_k,top_p", [
     ("bf16", 32000, 0.6, 20, 0.95), ("fp16", 999, 1.0, 0, 0.5), ("fp32", 2048, 1.0, 0, 1.0),
     ("bf16", 5000, 0.8, 700, 0.0),
 ])
@@ -121,15 +176,17 @@ def test_evaluate_posterior_filtered():
     np.testing.assert_array_equal(eos[:, 0].cpu().numpy(), (out == 7).any(1))
 
 
-def test_config5_shape_filtered_subset():
-    say("config-5 row shape (V=128256, k=5) with top_k=20, top_p=0.95: 24 requests")
+@pytest.mark.parametrize("top_k,top_p", [(20, 0.95), (0, 0.95), (2000, 0.0)])
+def test_config5_shape_filtered_subset(top_k, top_p):
+    say(f"config-5 row shape (V=128256, k=5) with top_k={top_k}, top_p={top_p}: 24 requests")
     c = stochastic_case(B=24, k=5, seed=1005)
     got = S.chain_speculative_sampling_from_logits(c.draft_logits.to(DEV), c.draft_tokens.to(DEV),
                                                    c.target_logits.to(DEV), 1.0,
-                                                   uniforms=c.uniforms.to(DEV), top_k=20,
-                                                   top_p=0.95)
+                                                   uniforms=c.uniforms.to(DEV), top_k=top_k,
+                                                   top_p=top_p)
     ref = OAc.chain_filtered(c.draft_logits.float().numpy(), c.draft_tokens.numpy(),
-                             c.target_logits.float().numpy(), 1.0, 20, 0.95, c.uniforms.numpy())
+                             c.target_logits.float().numpy(), 1.0, top_k, top_p,
+                             c.uniforms.numpy())
     for a, r in zip(got, ref):
         np.testing.assert_array_equal(a.cpu().numpy(), r)
 
