@@ -546,10 +546,11 @@ __device__ int ybin_first(RowsLds& L, const uint32_t* cnt, const uint64_t* mass,
 }
 
 // Counts (in ckey) and, with MASS, masses (in hist; else 0) of the elements per bin
-// (b0 < 0) or per sub-bin of bin b0, the last bin left out.
-template <int DT, bool MASS>
+// (SUB false; the last bin left out) or per sub-bin of bin b0, whose elements are those
+// in [xlo, xhi] (SUB true).
+template <int DT, bool MASS, bool SUB>
 __device__ void ybin_hist(RowsLds& L, const void* row, int64_t V, bool vec, float c, float neg,
-                          int b0) {
+                          int b0, float xlo, float xhi) {
   uint32_t* cnt = L.ckey;
   uint64_t* mass = reinterpret_cast<uint64_t*>(L.hist);
   for (int i = threadIdx.x; i < kYBins; i += kThreads) {
@@ -558,10 +559,15 @@ __device__ void ybin_hist(RowsLds& L, const void* row, int64_t V, bool vec, floa
   }
   __syncthreads();
   for_each_element<DT>(row, V, vec, [&](float x, int64_t) {
-    const float q = ypos(x, c, neg);
-    int b = ybin(q);
-    if (b == kYBins - 1 || (b0 >= 0 && b != b0)) return;
-    if (b0 >= 0) b = ysub(q, b0);
+    int b;
+    if constexpr (SUB) {
+      if (!(x >= xlo && x <= xhi)) return;
+      b = ysub(ypos(x, c, neg), b0);
+    } else {
+      const float q = ypos(x, c, neg);
+      if (!(q < (float)(kYBins - 1))) return;
+      b = (int)fmaxf(q, 0.0f);
+    }
     atomicAdd(&cnt[b], 1u);
     if constexpr (MASS) {
       const uint64_t m = fx40(canon::weight(x, c, neg));
@@ -569,6 +575,56 @@ __device__ void ybin_hist(RowsLds& L, const void* row, int64_t V, bool vec, floa
         atomicAdd(reinterpret_cast<unsigned long long*>(&mass[b]), (unsigned long long)m);
     }
   });
+  __syncthreads();
+}
+
+// The first key k in [lo, hi) with pred(k), pred non-decreasing in k and taken as true
+// at hi; hi if none.  The range is split 64 ways per step (one candidate per lane of
+// the calling wave), so a 32-bit range takes about 6 steps.  Wave-uniform.
+template <typename P>
+__device__ uint64_t wave_first_key(uint64_t lo, uint64_t hi, P&& pred) {
+  const uint64_t lane = threadIdx.x & 63;
+  while (lo < hi) {
+    const uint64_t step = (hi - lo + 63) / 64;
+    const uint64_t k = lo + lane * step;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(k >= hi || pred((uint32_t)k));
+    if (m == 0ull) {
+      lo += 63 * step + 1;  // false up to the last lane's key
+    } else {
+      const uint64_t f = (uint64_t)__builtin_ctzll(m);
+      if (f == 0) return lo;
+      const uint64_t nhi = lo + f * step < hi ? lo + f * step : hi;
+      lo += (f - 1) * step + 1;
+      hi = nhi;
+    }
+  }
+  return lo;
+}
+
+// Float range [xlo, xhi] of the keys of bin b0 (b1 < 0) or of its sub-bin b1: bins and
+// sub-bins are contiguous key ranges, found by two searches over the finite and
+// infinite keys.  Every thread calls it; the set must hold at least one key.
+__device__ void ybin_range(RowsLds& L, int b0, int b1, float c, float neg, float* xlo,
+                           float* xhi) {
+  float* xr = reinterpret_cast<float*>(L.part);
+  if (threadIdx.x < 64) {
+    const int target = b0 * kYBins + (b1 >= 0 ? b1 : 0);
+    auto pos = [&](uint32_t k) {
+      const float q = ypos(key_value(k), c, neg);
+      const int b = ybin(q);
+      return b * kYBins + (b1 >= 0 && b == b0 ? ysub(q, b0) : 0);
+    };
+    const uint64_t k_lo = okey(-INFINITY), k_end = (uint64_t)okey(INFINITY) + 1;
+    const uint64_t first = wave_first_key(k_lo, k_end, [&](uint32_t k) { return pos(k) <= target; });
+    const uint64_t past = wave_first_key(first, k_end, [&](uint32_t k) { return pos(k) < target; });
+    if (threadIdx.x == 0) {
+      xr[0] = key_value((uint32_t)first);
+      xr[1] = key_value((uint32_t)(past - 1));
+    }
+  }
+  __syncthreads();
+  *xlo = xr[0];
+  *xhi = xr[1];
   __syncthreads();
 }
 
@@ -585,23 +641,26 @@ template <int DT>
 __device__ bool ybin_threshold(RowsLds& L, const void* row, int64_t V, bool vec, float c,
                                float neg, bool use_k, bool use_p, int top_k, uint64_t target) {
   const int t = threadIdx.x;
-  if (use_p) ybin_hist<DT, true>(L, row, V, vec, c, neg, -1);
-  else ybin_hist<DT, false>(L, row, V, vec, c, neg, -1);
+  if (use_p) ybin_hist<DT, true, false>(L, row, V, vec, c, neg, -1, 0.f, 0.f);
+  else ybin_hist<DT, false, false>(L, row, V, vec, c, neg, -1, 0.f, 0.f);
   const int b0 = ybin_first(L, L.ckey, reinterpret_cast<const uint64_t*>(L.hist), kYBins - 1,
                             0u, 0ull, use_k, use_p, top_k, target);
   if (b0 < 0) return false;
   uint32_t base_c = L.above_c;
   uint64_t base_m = L.above_m;
   int b1 = -1;
+  float xlo, xhi;
   if (L.rcount > kCands) {
-    if (use_p) ybin_hist<DT, true>(L, row, V, vec, c, neg, b0);
-    else ybin_hist<DT, false>(L, row, V, vec, c, neg, b0);
+    ybin_range(L, b0, -1, c, neg, &xlo, &xhi);
+    if (use_p) ybin_hist<DT, true, true>(L, row, V, vec, c, neg, b0, xlo, xhi);
+    else ybin_hist<DT, false, true>(L, row, V, vec, c, neg, b0, xlo, xhi);
     b1 = ybin_first(L, L.ckey, reinterpret_cast<const uint64_t*>(L.hist), kYBins, base_c, base_m,
                     use_k, use_p, top_k, target);
     if (b1 < 0 || L.rcount > kCands) return false;
     base_c = L.above_c;
     base_m = L.above_m;
   }
+  ybin_range(L, b0, b1, c, neg, &xlo, &xhi);
   if (t == 0) {
     L.count = 0;
     L.zk = 0ull;
@@ -609,13 +668,10 @@ __device__ bool ybin_threshold(RowsLds& L, const void* row, int64_t V, bool vec,
   __syncthreads();
   uint64_t above = 0ull;  // top-k alone: the mass of the elements above the listed ones
   for_each_element<DT>(row, V, vec, [&](float x, int64_t) {
-    const float q = ypos(x, c, neg);
-    const int b = ybin(q);
-    const int sb = b1 >= 0 && b == b0 ? ysub(q, b0) : -1;
-    if (b == b0 && sb == b1) {
+    if (x >= xlo && x <= xhi) {
       const int slot = atomicAdd(&L.count, 1);
       if (slot < kCands) L.ckey[slot] = okey(x);
-    } else if (!use_p && (b < b0 || (b == b0 && sb < b1))) {
+    } else if (!use_p && x > xhi) {
       above += fx40(canon::weight(x, c, neg));
     }
   });
