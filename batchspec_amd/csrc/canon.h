@@ -59,7 +59,8 @@ constexpr float kC3 = 0x1.c91ce4p-5f;
 constexpr float kC4 = 0x1.277854p-7f;
 constexpr float kC5 = 0x1.e974f6p-10f;
 
-BSX_HD float exp2(float y) {
+// 2^y = ldexp(P(f), n): returns P(f) and sets n.
+BSX_HD float exp2_parts(float y, int* n_out) {
 #ifdef __HIP_DEVICE_COMPILE__
   float f;
   asm("v_fract_f32_e64 %0, %1 clamp" : "=v"(f) : "v"(y));
@@ -83,6 +84,13 @@ BSX_HD float exp2(float y) {
   p = fmaf(p, f, kC2);
   p = fmaf(p, f, kC1);
   p = fmaf(p, f, kC0);
+  *n_out = n;
+  return p;
+}
+
+BSX_HD float exp2(float y) {
+  int n;
+  const float p = exp2_parts(y, &n);
   return ldexpf(p, n);
 }
 

@@ -545,10 +545,25 @@ __device__ int ybin_first(RowsLds& L, const uint32_t* cnt, const uint64_t* mass,
   return first == INT_MAX ? -1 : first;
 }
 
-// Counts (in ckey) and, with MASS, masses (in hist; else 0) of the elements per bin
-// (SUB false; the last bin left out) or per sub-bin of bin b0, whose elements are those
-// in [xlo, xhi] (SUB true).
-template <int DT, bool MASS, bool SUB>
+// fx40(2^y) for y in (-41, 1): the 2^8 scale of fx40 folded into the exponent,
+// ldexp(P(f), n + 8) = ldexp(P(f), n) * 2^8 exactly (both normal), then its two
+// conversions.
+__device__ __forceinline__ uint64_t mass_of_exponent(float y) {
+  int n;
+  const float p = canon::exp2_parts(y, &n);
+  const float a = ldexpf(p, n + 8);
+  const uint32_t hi = (uint32_t)a;
+  const uint32_t lo = (uint32_t)((a - (float)hi) * 0x1p32f);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// What an exponent-bin histogram holds: counts (top-k on), fixed-point masses (top-p on).
+constexpr int kHistCount = 1, kHistMass = 2;
+
+// Counts (in ckey) and masses (in hist) of the elements per bin (SUB false; the last bin
+// left out) or per sub-bin of bin b0, whose elements are those in [xlo, xhi] (SUB true);
+// what MODE leaves out stays 0.
+template <int DT, int MODE, bool SUB>
 __device__ void ybin_hist(RowsLds& L, const void* row, int64_t V, bool vec, float c, float neg,
                           int b0, float xlo, float xhi) {
   uint32_t* cnt = L.ckey;
@@ -559,23 +574,30 @@ __device__ void ybin_hist(RowsLds& L, const void* row, int64_t V, bool vec, floa
   }
   __syncthreads();
   for_each_element<DT>(row, V, vec, [&](float x, int64_t) {
+    const float y = fmaf(x, c, neg);
+    const float q = -y * kYScale;  // ypos(x, c, neg)
     int b;
     if constexpr (SUB) {
       if (!(x >= xlo && x <= xhi)) return;
-      b = ysub(ypos(x, c, neg), b0);
+      b = ysub(q, b0);
     } else {
-      const float q = ypos(x, c, neg);
       if (!(q < (float)(kYBins - 1))) return;
       b = (int)fmaxf(q, 0.0f);
     }
-    atomicAdd(&cnt[b], 1u);
-    if constexpr (MASS) {
-      const uint64_t m = fx40(canon::weight(x, c, neg));
-      if (m != 0ull)
-        atomicAdd(reinterpret_cast<unsigned long long*>(&mass[b]), (unsigned long long)m);
-    }
+    if constexpr ((MODE & kHistCount) != 0) atomicAdd(&cnt[b], 1u);
+    if constexpr ((MODE & kHistMass) != 0)
+      atomicAdd(reinterpret_cast<unsigned long long*>(&mass[b]),
+                (unsigned long long)mass_of_exponent(y));
   });
   __syncthreads();
+}
+
+template <int DT, bool SUB>
+__device__ void ybin_hist_for(int mode, RowsLds& L, const void* row, int64_t V, bool vec, float c,
+                              float neg, int b0, float xlo, float xhi) {
+  if (mode == kHistCount) ybin_hist<DT, kHistCount, SUB>(L, row, V, vec, c, neg, b0, xlo, xhi);
+  else if (mode == kHistMass) ybin_hist<DT, kHistMass, SUB>(L, row, V, vec, c, neg, b0, xlo, xhi);
+  else ybin_hist<DT, kHistCount | kHistMass, SUB>(L, row, V, vec, c, neg, b0, xlo, xhi);
 }
 
 // The first key k in [lo, hi) with pred(k), pred non-decreasing in k and taken as true
@@ -629,20 +651,21 @@ __device__ void ybin_range(RowsLds& L, int b0, int b1, float c, float neg, float
 }
 
 // Threshold of a row whose upper set is too large to list: the first log2-weight bin
-// (one histogram pass) at which the running count / mass reaches the target, a
-// histogram of its sub-bins when it holds more than kCands elements (a second pass),
-// then the elements of that bin (sub-bin) listed and walked with what lies above as the
-// base; a listed bin with more than kThreads elements is narrowed to one of its
-// sub-bins first (in LDS).  For top-k alone the histograms count only, and the listing
-// pass sums the masses above.  The row gets no list.  Returns false (in every thread)
-// when the threshold is not found this way (a bin too dense, or a target beyond the
-// mass of the bins).  Needs a finite row max.
+// (one histogram pass) at which the running count / mass reaches the target, then the
+// elements of that bin listed and walked with what lies above as the base.  A bin of
+// more than kCands elements is narrowed to one of its 1024 sub-bins by a histogram of
+// them (a second pass) before it is listed; a listed bin of more than kThreads elements
+// is narrowed to one of its sub-bins in LDS.  The histograms hold counts for top-k
+// (for top-k alone the listing pass then sums the masses above) and masses for top-p
+// (for top-p alone a bin is known to be too large only once listed).  The row gets no
+// list.  Returns false (in every thread) when the threshold is not found this way (a
+// sub-bin too dense, or a target beyond the mass of the bins).  Needs a finite row max.
 template <int DT>
 __device__ bool ybin_threshold(RowsLds& L, const void* row, int64_t V, bool vec, float c,
                                float neg, bool use_k, bool use_p, int top_k, uint64_t target) {
   const int t = threadIdx.x;
-  if (use_p) ybin_hist<DT, true, false>(L, row, V, vec, c, neg, -1, 0.f, 0.f);
-  else ybin_hist<DT, false, false>(L, row, V, vec, c, neg, -1, 0.f, 0.f);
+  const int mode = (use_k ? kHistCount : 0) | (use_p ? kHistMass : 0);
+  ybin_hist_for<DT, false>(mode, L, row, V, vec, c, neg, -1, 0.f, 0.f);
   const int b0 = ybin_first(L, L.ckey, reinterpret_cast<const uint64_t*>(L.hist), kYBins - 1,
                             0u, 0ull, use_k, use_p, top_k, target);
   if (b0 < 0) return false;
@@ -650,38 +673,50 @@ __device__ bool ybin_threshold(RowsLds& L, const void* row, int64_t V, bool vec,
   uint64_t base_m = L.above_m;
   int b1 = -1;
   float xlo, xhi;
-  if (L.rcount > kCands) {
+  // narrows bin b0 to the sub-bin b1 that holds the threshold
+  auto narrow = [&]() -> bool {
     ybin_range(L, b0, -1, c, neg, &xlo, &xhi);
-    if (use_p) ybin_hist<DT, true, true>(L, row, V, vec, c, neg, b0, xlo, xhi);
-    else ybin_hist<DT, false, true>(L, row, V, vec, c, neg, b0, xlo, xhi);
-    b1 = ybin_first(L, L.ckey, reinterpret_cast<const uint64_t*>(L.hist), kYBins, base_c, base_m,
-                    use_k, use_p, top_k, target);
-    if (b1 < 0 || L.rcount > kCands) return false;
+    ybin_hist_for<DT, true>(mode, L, row, V, vec, c, neg, b0, xlo, xhi);
+    b1 = ybin_first(L, L.ckey, reinterpret_cast<const uint64_t*>(L.hist), kYBins, base_c,
+                    base_m, use_k, use_p, top_k, target);
+    if (b1 < 0 || (use_k && L.rcount > kCands)) return false;
     base_c = L.above_c;
     base_m = L.above_m;
-  }
-  ybin_range(L, b0, b1, c, neg, &xlo, &xhi);
-  if (t == 0) {
-    L.count = 0;
-    L.zk = 0ull;
-  }
-  __syncthreads();
-  uint64_t above = 0ull;  // top-k alone: the mass of the elements above the listed ones
-  for_each_element<DT>(row, V, vec, [&](float x, int64_t) {
-    if (x >= xlo && x <= xhi) {
-      const int slot = atomicAdd(&L.count, 1);
-      if (slot < kCands) L.ckey[slot] = okey(x);
-    } else if (!use_p && x > xhi) {
-      above += fx40(canon::weight(x, c, neg));
+    return true;
+  };
+  // lists the elements of bin b0 (sub-bin b1)
+  auto list = [&]() {
+    ybin_range(L, b0, b1, c, neg, &xlo, &xhi);
+    if (t == 0) {
+      L.count = 0;
+      L.zk = 0ull;
     }
-  });
-  if (!use_p) {
-    above = wave_sum_u64(above);
-    if ((t & 63) == 0 && above != 0ull)
-      atomicAdd(reinterpret_cast<unsigned long long*>(&L.zk), (unsigned long long)above);
+    __syncthreads();
+    uint64_t above = 0ull;  // top-k alone: the mass of the elements above the listed ones
+    for_each_element<DT>(row, V, vec, [&](float x, int64_t) {
+      if (x >= xlo && x <= xhi) {
+        const int slot = atomicAdd(&L.count, 1);
+        if (slot < kCands) L.ckey[slot] = okey(x);
+      } else if (!use_p && x > xhi) {
+        above += mass_of_exponent(fmaf(x, c, neg));
+      }
+    });
+    if (!use_p) {
+      above = wave_sum_u64(above);
+      if ((t & 63) == 0 && above != 0ull)
+        atomicAdd(reinterpret_cast<unsigned long long*>(&L.zk), (unsigned long long)above);
+    }
+    __syncthreads();
+    if (!use_p) base_m = L.zk;
+  };
+  if (use_k && L.rcount > kCands && !narrow()) return false;
+  list();
+  if (!use_k && L.count > kCands) {
+    // a bin of uncounted elements (top-p alone) too large to list
+    __syncthreads();
+    if (!narrow()) return false;
+    list();
   }
-  __syncthreads();
-  if (!use_p) base_m = L.zk;
   int n = L.count;
   if (n > kCands) return false;
   if (n > kThreads && b1 < 0) {
