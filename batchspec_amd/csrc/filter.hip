@@ -33,18 +33,21 @@
 //     1. the canonical (M, Z) pass lists candidates on the way: the k-th largest of
 //        the maxima of 2048 disjoint groups (read first) bounds t* from below; groups
 //        are listed only when their maximum reaches it (for top-p alone the bound of
-//        rank 64 is used);
-//     2. with at most kCands candidates, each gets the count and mass of the listed
-//        keys at or above its own (every element of the row there is listed), which
-//        gives t* and Z_K exactly, and the kept indices are written out;
-//     3. if the list overflowed (or the row is too short for step 1), the bound of all
+//        rank 64 is used); with at most kCands candidates, each gets the count and
+//        mass of the listed keys at or above its own (every element of the row there
+//        is listed), which gives t* and Z_K exactly, and the kept indices are written
+//        out;
+//     2. if the list overflowed (or the row is too short for step 1), the bound of all
 //        2048 lane maxima and a second read of the row list the candidates again;
-//     4. if that fails too (a top_k above kCands, a nucleus below the bound), a
-//        histogram of counts and masses over 1024 bins of the weight's exponent picks
-//        the bin that holds t*; its elements (or, for a bin of more than kCands, those
-//        of one of its 1024 sub-bins, after a histogram of them) are listed and walked
-//        with the count and mass above them as the base; the row gets no list;
-//     5. if a sub-bin is still too dense (ties), an exact radix select over the key
+//     a row that neither lists (a top_k above kCands, a nucleus below the bound) is
+//     left, for top-p alone or a top_k above kDeferTopK, to
+//   filter_deferred_kernel: one workgroup per row, the others leave at once;
+//     otherwise (rare: ties) it takes step 4 in place.
+//     3. a histogram of counts and masses over 1024 bins of the weight's exponent
+//        picks the bin that holds t*; its elements (or, for a bin of more than kCands,
+//        those of one of its 1024 sub-bins, after a histogram of them) are listed and
+//        walked with the count and mass above them as the base; the row gets no list;
+//     4. if a sub-bin is still too dense (ties), an exact radix select over the key
 //        bits, 8 per pass, with counts and fixed-point masses per digit in LDS.
 //   filter_tiles_kernel: (request, part) workgroups: the ratio tests, then, when the
 //     row the chain stops at has no kept list, the fixed-point sums of its draw weights
@@ -75,6 +78,7 @@ constexpr int kThreads = 256;
 constexpr int kCands = 1024;      // candidates listed in LDS per row
 constexpr int kCap = 256;         // kept elements listed per row for the draw
 constexpr int kTopPProbe = 64;    // rank of the lane-maximum bound for top-p alone
+constexpr int kDeferTopK = 64;    // top_k above which unlisted rows go to the second kernel
 constexpr int kMaxTiles = 2048;   // tiles of a whole-row draw
 constexpr int kBinShift = 21;     // 11-bit key bins for the bound
 constexpr int kBins = 1 << (32 - kBinShift);
@@ -109,7 +113,10 @@ struct RowsArgs {
   float top_p;    // <= 0 or >= 1: off
   RowInfo* info;
   int32_t* lists; // [rows][kCap]
+  int defer;      // rows that list neither go to filter_deferred_kernel (else step 4 here)
 };
+
+constexpr int32_t kDeferred = -2;  // n_list of a row whose threshold is not found yet
 
 __device__ __forceinline__ bool reached(bool use_k, bool use_p, uint32_t cnt, uint64_t mass,
                                         int top_k, uint64_t target) {
@@ -370,7 +377,7 @@ struct Collector {
 // keys at or above its own; t* is the largest key that reaches the target.  Writes the
 // kept indices (at most kCap, else the row gets no list; no list either when list_out
 // is null).  Returns false (in every thread) when no listed key reaches the target.
-__device__ bool walk(RowsLds& L, int n, float c, float neg, bool use_k, bool use_p, int top_k,
+__device__ __forceinline__ bool walk(RowsLds& L, int n, float c, float neg, bool use_k, bool use_p, int top_k,
                      uint64_t target, int32_t* list_out, uint32_t base_c = 0u,
                      uint64_t base_m = 0ull) {
   typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
@@ -489,7 +496,7 @@ __device__ __forceinline__ int ysub(float q, int b) {
 // count / mass of cnt / mass reaches the threshold.  Returns it (-1 if none does) and
 // leaves what lies above it in L.above_c / L.above_m and its own count in L.rcount.
 // Uses part.  Every thread calls it.
-__device__ int ybin_first(RowsLds& L, const uint32_t* cnt, const uint64_t* mass, int nb,
+__device__ __forceinline__ int ybin_first(RowsLds& L, const uint32_t* cnt, const uint64_t* mass, int nb,
                           uint32_t base_c, uint64_t base_m, bool use_k, bool use_p, int top_k,
                           uint64_t target) {
   constexpr int PER = kYBins / kThreads;
@@ -661,7 +668,7 @@ __device__ void ybin_range(RowsLds& L, int b0, int b1, float c, float neg, float
 // list.  Returns false (in every thread) when the threshold is not found this way (a
 // sub-bin too dense, or a target beyond the mass of the bins).  Needs a finite row max.
 template <int DT>
-__device__ bool ybin_threshold(RowsLds& L, const void* row, int64_t V, bool vec, float c,
+__device__ __forceinline__ bool ybin_threshold(RowsLds& L, const void* row, int64_t V, bool vec, float c,
                                float neg, bool use_k, bool use_p, int top_k, uint64_t target) {
   const int t = threadIdx.x;
   const int mode = (use_k ? kHistCount : 0) | (use_p ? kHistMass : 0);
@@ -758,6 +765,94 @@ __device__ bool ybin_threshold(RowsLds& L, const void* row, int64_t V, bool vec,
     n = L.count;
   }
   return walk(L, n, c, neg, use_k, use_p, top_k, target, nullptr, base_c, base_m);
+}
+
+// Step 4: exact radix select over the key bits, 8 per pass, counts and fixed-point
+// masses per digit in LDS.  Leaves t* in L.tk, Z_K in L.zk, no list.
+template <int DT>
+__device__ __forceinline__ void radix_threshold(RowsLds& L, const void* row, int64_t V, bool vec, float c,
+                                float neg, bool use_k, bool use_p, int top_k, uint64_t target) {
+  const int t = threadIdx.x;
+  uint32_t* hc = L.hist;                                     // [256]
+  uint64_t* hm = reinterpret_cast<uint64_t*>(L.hist + 256);  // [256]
+  constexpr int NP = radix_passes<DT>();
+  if (t == 0) {
+    L.prefix = 0u;
+    L.above_c = 0u;
+    L.above_m = 0ull;
+  }
+  for (int pass = 0; pass < NP; ++pass) {
+    const int shift = 24 - 8 * pass;
+    hc[t] = 0u;
+    hm[t] = 0ull;
+    __syncthreads();
+    const uint32_t prefix = L.prefix;
+    for_each_element<DT>(row, V, vec, [&](float x, int64_t) {
+      const uint32_t key = okey(x);
+      if (pass == 0 || (key >> (shift + 8)) == prefix) {
+        const uint32_t d = (key >> shift) & 255u;
+        atomicAdd(&hc[d], 1u);
+        const uint64_t m = fx40(canon::weight(x, c, neg));
+        if (m != 0ull)
+          atomicAdd(reinterpret_cast<unsigned long long*>(&hm[d]), (unsigned long long)m);
+      }
+    });
+    __syncthreads();
+    if (t == 0) {
+      uint32_t cum_c = L.above_c;
+      uint64_t cum_m = L.above_m;
+      int chosen = -1;
+      uint32_t ch_prev_c = 0u;
+      uint64_t ch_prev_m = 0ull, ch_m = 0ull;
+      for (int d = 255; d >= 0; --d) {
+        if (hc[d] == 0u) continue;
+        const uint32_t pc = cum_c;
+        const uint64_t pm = cum_m;
+        cum_c += hc[d];
+        cum_m += hm[d];
+        chosen = d;  // the lowest non-empty digit so far
+        ch_prev_c = pc;
+        ch_prev_m = pm;
+        ch_m = cum_m;
+        if (reached(use_k, use_p, cum_c, cum_m, top_k, target)) break;
+      }
+      L.prefix = (pass == 0 ? 0u : (prefix << 8)) | (uint32_t)chosen;
+      L.above_c = ch_prev_c;
+      L.above_m = ch_prev_m;
+      L.zk = ch_m;
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    constexpr int low_bits = 32 - 8 * NP;
+    uint32_t tk = low_bits == 0 ? L.prefix : (L.prefix << low_bits);
+    // the bits below the varying ones are 0 for positive values, 1 for negative
+    if (low_bits > 0 && !(tk & 0x80000000u)) tk |= (1u << low_bits) - 1u;
+    L.tk = tk;
+    L.nk = -1;
+  }
+  __syncthreads();
+}
+
+// Steps 3 and 4 for a row whose upper set could not be listed.
+template <int DT>
+__device__ __forceinline__ void large_threshold(RowsLds& L, const void* row, int64_t V, bool vec, float c,
+                                float neg, bool use_k, bool use_p, int top_k, uint64_t target) {
+  bool found = false;
+  if (neg > -INFINITY && neg < INFINITY)
+    found = ybin_threshold<DT>(L, row, V, vec, c, neg, use_k, use_p, top_k, target);
+  if (!found) radix_threshold<DT>(L, row, V, vec, c, neg, use_k, use_p, top_k, target);
+}
+
+__device__ __forceinline__ void write_info(RowsLds& L, RowInfo* info, float M) {
+  if (threadIdx.x == 0) {
+    RowInfo ri;
+    ri.m = M;
+    ri.inv_k = 1.0f / (canon::u64_to_f32(L.zk) * 0x1p-40f);
+    ri.t_key = L.tk;
+    ri.n_list = L.nk;
+    *info = ri;
+  }
 }
 
 template <int DT>
@@ -877,81 +972,38 @@ __global__ void __launch_bounds__(kThreads) filter_rows_kernel(RowsArgs a) {
     }
   }
 
-  // 3. log2-weight bins
-  if (!listed && neg > -INFINITY && neg < INFINITY)
-    listed = ybin_threshold<DT>(L, row, V, vec, c, neg, use_k, use_p, a.top_k, target);
-
-  // 4. exact radix select
-  if (!listed) {
-    uint32_t* hc = L.hist;                                     // [256]
-    uint64_t* hm = reinterpret_cast<uint64_t*>(L.hist + 256);  // [256]
-    constexpr int NP = radix_passes<DT>();
-    if (t == 0) {
-      L.prefix = 0u;
-      L.above_c = 0u;
-      L.above_m = 0ull;
-    }
-    for (int pass = 0; pass < NP; ++pass) {
-      const int shift = 24 - 8 * pass;
-      hc[t] = 0u;
-      hm[t] = 0ull;
-      __syncthreads();
-      const uint32_t prefix = L.prefix;
-      for_each_element<DT>(row, V, vec, [&](float x, int64_t) {
-        const uint32_t key = okey(x);
-        if (pass == 0 || (key >> (shift + 8)) == prefix) {
-          const uint32_t d = (key >> shift) & 255u;
-          atomicAdd(&hc[d], 1u);
-          const uint64_t m = fx40(canon::weight(x, c, neg));
-          if (m != 0ull)
-            atomicAdd(reinterpret_cast<unsigned long long*>(&hm[d]), (unsigned long long)m);
-        }
-      });
-      __syncthreads();
-      if (t == 0) {
-        uint32_t cum_c = L.above_c;
-        uint64_t cum_m = L.above_m;
-        int chosen = -1;
-        uint32_t ch_prev_c = 0u;
-        uint64_t ch_prev_m = 0ull, ch_m = 0ull;
-        for (int d = 255; d >= 0; --d) {
-          if (hc[d] == 0u) continue;
-          const uint32_t pc = cum_c;
-          const uint64_t pm = cum_m;
-          cum_c += hc[d];
-          cum_m += hm[d];
-          chosen = d;  // the lowest non-empty digit so far
-          ch_prev_c = pc;
-          ch_prev_m = pm;
-          ch_m = cum_m;
-          if (reached(use_k, use_p, cum_c, cum_m, a.top_k, target)) break;
-        }
-        L.prefix = (pass == 0 ? 0u : (prefix << 8)) | (uint32_t)chosen;
-        L.above_c = ch_prev_c;
-        L.above_m = ch_prev_m;
-        L.zk = ch_m;
-      }
-      __syncthreads();
-    }
-    if (t == 0) {
-      constexpr int low_bits = 32 - 8 * NP;
-      uint32_t tk = low_bits == 0 ? L.prefix : (L.prefix << low_bits);
-      // the bits below the varying ones are 0 for positive values, 1 for negative
-      if (low_bits > 0 && !(tk & 0x80000000u)) tk |= (1u << low_bits) - 1u;
-      L.tk = tk;
-      L.nk = -1;
-    }
-    __syncthreads();
+  if (!listed && a.defer) {
+    // steps 3 and 4 in filter_deferred_kernel (kept out of this kernel, whose registers
+    // bound how many rows it holds at once)
+    if (t == 0) a.info[r] = RowInfo{M, Z, 0u, kDeferred};
+    return;
   }
+  if (!listed) radix_threshold<DT>(L, row, V, vec, c, neg, use_k, use_p, a.top_k, target);
+  write_info(L, a.info + r, M);
+}
 
-  if (t == 0) {
-    RowInfo ri;
-    ri.m = M;
-    ri.inv_k = 1.0f / (canon::u64_to_f32(L.zk) * 0x1p-40f);
-    ri.t_key = L.tk;
-    ri.n_list = L.nk;
-    a.info[r] = ri;
-  }
+// Steps 3 and 4 of the rows filter_rows_kernel could not list (their statistics in the
+// row info: M, and Z in place of 1 / Z_K); the other rows are left as they are.  Its
+// registers let the device hold every row at once.
+template <int DT>
+__global__ void __launch_bounds__(kThreads) filter_deferred_kernel(RowsArgs a) {
+  __shared__ __align__(16) RowsLds L;
+  const int64_t r = blockIdx.x;
+  const RowInfo ri = a.info[r];
+  if (ri.n_list != kDeferred) return;
+  const int64_t V = a.V;
+  const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
+  const char* row = r < a.n_a ? static_cast<const char*>(a.a) + r * V * esz
+                              : static_cast<const char*>(a.b) + (r - a.n_a) * V * esz;
+  const bool vec = ((V * esz) % 16 == 0) && (((uintptr_t)row) % 16 == 0);
+  const float c = a.c;
+  const bool use_k = a.top_k > 0 && (int64_t)a.top_k < V;
+  const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
+  const float M = ri.m, Z = ri.inv_k;
+  const float neg = -(M * c);
+  const uint64_t target = use_p ? (uint64_t)ceilf((a.top_p * Z) * 0x1p40f) : 0ull;
+  large_threshold<DT>(L, row, V, vec, c, neg, use_k, use_p, a.top_k, target);
+  write_info(L, a.info + r, M);
 }
 
 // ----------------------------------------------------------------------------
@@ -1383,9 +1435,20 @@ static int launch_filter_rows(const void* a, int64_t n_a, const void* b, int64_t
   ra.info = static_cast<filt::RowInfo*>(ws);
   ra.lists = reinterpret_cast<int32_t*>(static_cast<char*>(ws) +
                                         filt::align256((n_a + n_b) * (int64_t)sizeof(filt::RowInfo)));
+  // Top-p alone and a top_k above kDeferTopK expect rows whose upper set cannot be
+  // listed: those finish in filter_deferred_kernel.  Below it such rows (ties) are rare
+  // and take the radix select in place, without a second launch.
+  const bool use_k = top_k > 0 && (int64_t)top_k < V;
+  const bool use_p = top_p > 0.f && top_p < 1.f;
+  ra.defer = (use_p && !use_k) || (use_k && top_k > filt::kDeferTopK);
   hipLaunchKernelGGL((filt::filter_rows_kernel<DT>), dim3((unsigned)(n_a + n_b)),
                      dim3(filt::kThreads), 0, st, ra);
   BSX_LAUNCH_CHECK();
+  if (ra.defer) {
+    hipLaunchKernelGGL((filt::filter_deferred_kernel<DT>), dim3((unsigned)(n_a + n_b)),
+                       dim3(filt::kThreads), 0, st, ra);
+    BSX_LAUNCH_CHECK();
+  }
   return BSX_OK;
 }
 
