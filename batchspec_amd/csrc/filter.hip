@@ -51,7 +51,7 @@
 //        bits, 8 per pass, with counts and fixed-point masses per digit in LDS.
 //   filter_tiles_kernel: (request, part) workgroups: the ratio tests, then, when the
 //     row the chain stops at has no kept list, the fixed-point sums of its draw weights
-//     over wave-sized tiles of the row, 16 tiles per workgroup;
+//     over wave-sized tiles of the row, 8 tiles per workgroup;
 //   filter_chain_kernel: one workgroup per request: the ratio tests, then the draw
 //     from the row the chain stops at, over its kept list, or from the tile sums (their
 //     prefix, the tile, the lane, the element) without one.
@@ -1027,7 +1027,7 @@ struct ChainArgs {
 
 // Tiles of a whole-row draw: 64 lanes x E consecutive elements (E a multiple of 8), at
 // most kMaxTiles of them; filter_tiles_kernel sums kTilesPerPart per workgroup.
-constexpr int kTilesPerPart = 16;
+constexpr int kTilesPerPart = 8;
 static_assert(kTilesPerPart % (kThreads / 64) == 0, "whole tiles per wave");
 __host__ __device__ inline int draw_tile_elems(int64_t V) {
   return kGroup * (int)ceil_div(V, (int64_t)kMaxTiles * 64 * kGroup);
@@ -1232,6 +1232,7 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
   __shared__ uint64_t lr[kCap];
   __shared__ uint64_t s_acc, s_tbase;
   __shared__ uint64_t excl[kThreads];
+  __shared__ uint64_t s_wave[kThreads / 64];
   __shared__ uint64_t tsum[kMaxTiles];
   const int b = blockIdx.x;
   const int t = threadIdx.x;
@@ -1301,19 +1302,16 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
         const int T = t * (kMaxTiles / kThreads) + i;
         if (T < ntiles) mine += tsum[T];
       }
-      excl[t] = mine;
+      const uint64_t incl = wave_prefix_u64(mine);
+      if (lane == 63) s_wave[wave] = incl;
       __syncthreads();
-      if (t == 0) {
-        uint64_t run = 0ull;
-        for (int i = 0; i < kThreads; ++i) {
-          const uint64_t x = excl[i];
-          excl[i] = run;
-          run += x;
-        }
-        s_acc = run;
+      uint64_t off = 0ull;
+      total = 0ull;
+      for (int w = 0; w < kThreads / 64; ++w) {
+        if (w < wave) off += s_wave[w];
+        total += s_wave[w];
       }
-      __syncthreads();
-      total = s_acc;
+      excl[t] = off + (incl - mine);
       __syncthreads();
       if (total != 0ull) break;
     }
