@@ -230,3 +230,38 @@ def test_randomized_filtered_chains():
             np.testing.assert_array_equal(a.cpu().numpy(), r, err_msg=f"case {case}: {dt} onehot="
                                           f"{onehot} B={B} k={k} V={V} T={T} top_k={top_k} "
                                           f"top_p={top_p} sigma={sigma} q={q}")
+
+
+def test_randomized_large_thresholds():
+    """30 random rows sets on the paths for upper sets too large to list (top-p alone,
+    top_k above 64): N(0, sigma) rows, some with -inf padding, ties from quantisation or a
+    dense band of values, ragged lengths and the three logit types; the filtered
+    probabilities bit-exact against the oracle."""
+    say("get_sampling_probs: 30 randomized large-threshold cases")
+    rng = np.random.default_rng(77)
+    for case in range(30):
+        dt = ["bf16", "fp16", "fp32"][int(rng.integers(3))]
+        V = int(rng.choice([1500, 4099, 20000, 65537]))
+        T = float(rng.choice([0.5, 1.0, 2.0]))
+        if rng.random() < 0.5:
+            top_k, top_p = 0, float(rng.choice([0.3, 0.9, 0.99, 0.9999]))
+        else:
+            top_k = int(rng.choice([65, 300, 1500, V // 2]))
+            top_p = float(rng.choice([0.0, 0.9, 0.99]))
+        sigma = float(rng.choice([0.5, 2.0, 6.0]))
+        x = rng.standard_normal((2, V)) * sigma
+        kind = rng.choice(["plain", "quantized", "band", "padded"])
+        if kind == "quantized":
+            x = np.round(x * 4) / 4
+        elif kind == "band":
+            idx = rng.choice(V, V // 4, replace=False)
+            x[:, idx] = 1.0 + 0.01 * rng.random((2, V // 4))
+        elif kind == "padded":
+            x[:, -(V // 10):] = -np.inf
+        xt = torch.from_numpy(x.astype(np.float32)).to(DT[dt])
+        got = S.get_sampling_probs(xt.to(DEV), top_p=top_p, top_k=top_k, temperature=T)
+        ref = OAc.filtered_probs(xt.float().numpy(), T, top_k, top_p)
+        np.testing.assert_array_equal(
+            got.cpu().numpy().reshape(ref.shape).view(np.int32), ref.view(np.int32),
+            err_msg=f"case {case}: {dt} V={V} T={T} top_k={top_k} top_p={top_p} sigma={sigma} "
+                    f"kind={kind}")
