@@ -377,9 +377,9 @@ struct Collector {
 // keys at or above its own; t* is the largest key that reaches the target.  Writes the
 // kept indices (at most kCap, else the row gets no list; no list either when list_out
 // is null).  Returns false (in every thread) when no listed key reaches the target.
-__device__ __forceinline__ bool walk(RowsLds& L, int n, float c, float neg, bool use_k, bool use_p, int top_k,
-                     uint64_t target, int32_t* list_out, uint32_t base_c = 0u,
-                     uint64_t base_m = 0ull) {
+__device__ __forceinline__ bool walk(RowsLds& L, int n, float c, float neg, bool use_k,
+                                     bool use_p, int top_k, uint64_t target, int32_t* list_out,
+                                     uint32_t base_c = 0u, uint64_t base_m = 0ull) {
   typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
   const int t = threadIdx.x;
   uint64_t* cm = reinterpret_cast<uint64_t*>(L.hist);
@@ -496,9 +496,9 @@ __device__ __forceinline__ int ysub(float q, int b) {
 // count / mass of cnt / mass reaches the threshold.  Returns it (-1 if none does) and
 // leaves what lies above it in L.above_c / L.above_m and its own count in L.rcount.
 // Uses part.  Every thread calls it.
-__device__ __forceinline__ int ybin_first(RowsLds& L, const uint32_t* cnt, const uint64_t* mass, int nb,
-                          uint32_t base_c, uint64_t base_m, bool use_k, bool use_p, int top_k,
-                          uint64_t target) {
+__device__ __forceinline__ int ybin_first(RowsLds& L, const uint32_t* cnt, const uint64_t* mass,
+                                          int nb, uint32_t base_c, uint64_t base_m, bool use_k,
+                                          bool use_p, int top_k, uint64_t target) {
   constexpr int PER = kYBins / kThreads;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   uint32_t cc[PER];
@@ -668,8 +668,9 @@ __device__ void ybin_range(RowsLds& L, int b0, int b1, float c, float neg, float
 // list.  Returns false (in every thread) when the threshold is not found this way (a
 // sub-bin too dense, or a target beyond the mass of the bins).  Needs a finite row max.
 template <int DT>
-__device__ __forceinline__ bool ybin_threshold(RowsLds& L, const void* row, int64_t V, bool vec, float c,
-                               float neg, bool use_k, bool use_p, int top_k, uint64_t target) {
+__device__ __forceinline__ bool ybin_threshold(
+    RowsLds& L, const void* row, int64_t V, bool vec, float c, float neg, bool use_k,
+    bool use_p, int top_k, uint64_t target) {
   const int t = threadIdx.x;
   const int mode = (use_k ? kHistCount : 0) | (use_p ? kHistMass : 0);
   ybin_hist_for<DT, false>(mode, L, row, V, vec, c, neg, -1, 0.f, 0.f);
@@ -770,8 +771,9 @@ __device__ __forceinline__ bool ybin_threshold(RowsLds& L, const void* row, int6
 // Step 4: exact radix select over the key bits, 8 per pass, counts and fixed-point
 // masses per digit in LDS.  Leaves t* in L.tk, Z_K in L.zk, no list.
 template <int DT>
-__device__ __forceinline__ void radix_threshold(RowsLds& L, const void* row, int64_t V, bool vec, float c,
-                                float neg, bool use_k, bool use_p, int top_k, uint64_t target) {
+__device__ __forceinline__ void radix_threshold(
+    RowsLds& L, const void* row, int64_t V, bool vec, float c, float neg, bool use_k,
+    bool use_p, int top_k, uint64_t target) {
   const int t = threadIdx.x;
   uint32_t* hc = L.hist;                                     // [256]
   uint64_t* hm = reinterpret_cast<uint64_t*>(L.hist + 256);  // [256]
@@ -836,8 +838,9 @@ __device__ __forceinline__ void radix_threshold(RowsLds& L, const void* row, int
 
 // Steps 3 and 4 for a row whose upper set could not be listed.
 template <int DT>
-__device__ __forceinline__ void large_threshold(RowsLds& L, const void* row, int64_t V, bool vec, float c,
-                                float neg, bool use_k, bool use_p, int top_k, uint64_t target) {
+__device__ __forceinline__ void large_threshold(
+    RowsLds& L, const void* row, int64_t V, bool vec, float c, float neg, bool use_k,
+    bool use_p, int top_k, uint64_t target) {
   bool found = false;
   if (neg > -INFINITY && neg < INFINITY)
     found = ybin_threshold<DT>(L, row, V, vec, c, neg, use_k, use_p, top_k, target);
