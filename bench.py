@@ -17,7 +17,9 @@ Printed: one JSON line with
               bytes per pass and `mfma_util` the matrix-core use of the attention
               kernel, both from the committed rocprofv3 counter summaries (profiles/)
   greedy_accept / stochastic_accept   acceptance at [64, 5, 128256] (config-2 shape)
-              and config 5 (B=128, k=5, V=128256), time and HBM fraction
+              and config 5 (B=128, k=5, V=128256), time and HBM fraction;
+              stochastic_accept_top_k20_top_p095 / stochastic_accept_top_p095 the
+              same with the reference's default filters, and with top-p alone
   config4_tree_attention / config3b_verify_attention / config3a_draft_attention
               verify attention at the other BASELINE configurations (config 4 also
               `spaced`: the same runs separated by short idle gaps, which keep the
