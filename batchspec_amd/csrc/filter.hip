@@ -217,7 +217,7 @@ __device__ __forceinline__ uint32_t wave_suffix_u32(uint32_t v) {
 // Bin (11-bit key prefix) holding the k-th largest of the 2048 values lm (8 per
 // thread); -1 if k > 2048.  L.above receives the number of values in higher bins.
 // Every thread of the workgroup calls it.
-__device__ int kth_bin(RowsLds& L, const float (&lm)[8], int k) {
+__device__ __forceinline__ int kth_bin(RowsLds& L, const float (&lm)[8], int k) {
   constexpr int PER = kBins / kThreads;  // bins summed per thread
   const int t = threadIdx.x;
   u32x4* h4 = reinterpret_cast<u32x4*>(L.hist);
@@ -266,7 +266,7 @@ __device__ int kth_bin(RowsLds& L, const float (&lm)[8], int k) {
 // Key of the k-th largest of the 2048 values lm (k <= 2048), exact when at most
 // kThreads of them share its 12-bit bin (else the bin's lower edge, a smaller bound);
 // 0 when that value is -inf or k > 2048.  Uses hist and part.  Every thread calls it.
-__device__ uint32_t kth_key(RowsLds& L, const float (&lm)[8], int k) {
+__device__ __forceinline__ uint32_t kth_key(RowsLds& L, const float (&lm)[8], int k) {
   const int t = threadIdx.x;
   const int bin = kth_bin(L, lm, k);
   if (bin < kFirstFiniteBin) return 0u;
@@ -299,6 +299,15 @@ __device__ uint32_t kth_key(RowsLds& L, const float (&lm)[8], int k) {
   }
   __syncthreads();
   return result;
+}
+
+// kth_key as a call: for the statistics pass's first round, where inlining it would raise
+// the pass's registers (and with them the rows a compute unit holds).  The values go by
+// value, in registers (an array by reference would go through scratch memory).
+__device__ __noinline__ uint32_t kth_key_call(RowsLds& L, float v0, float v1, float v2, float v3,
+                                              float v4, float v5, float v6, float v7, int k) {
+  const float lm[8] = {v0, v1, v2, v3, v4, v5, v6, v7};
+  return kth_key(L, lm, k);
 }
 
 // The 8 elements of a complete group of a row with 16-byte aligned groups.
@@ -350,7 +359,8 @@ struct Collector {
   // disjoint, so the k-th largest of the 2048 has at least k elements of the row at or
   // above it, and so has t*.
   __device__ void first(const float (&gm)[8]) {
-    const uint32_t kb = kth_key(*L, gm, k);
+    const uint32_t kb =
+        kth_key_call(*L, gm[0], gm[1], gm[2], gm[3], gm[4], gm[5], gm[6], gm[7], k);
     if (kb == 0u) on = false;
     else lf = key_value(kb);
   }
@@ -957,11 +967,12 @@ __global__ void __launch_bounds__(kThreads) filter_rows_kernel(RowsArgs a) {
 
   bool listed = false;
   const bool early = col.on && L.count <= kCands;
-  if (early) listed = walk(L, L.count, c, neg, use_k, use_p, a.top_k, target, list_out);
-
-  // 2. otherwise the bound of all lane maxima, and a second read of the row (a list
-  //    cannot hold more than kCands of the top-k)
-  if (!listed && !early && k_eff <= kCands) {
+  if (early) {
+    listed = walk(L, L.count, c, neg, use_k, use_p, a.top_k, target, list_out);
+  } else if (k_eff <= kCands) {
+    // 2. otherwise the bound of all lane maxima, and a second read of the row (a list
+    //    cannot hold more than kCands of the top-k).  On this branch only, so that the
+    //    lane maxima need not stay live across the walk above.
     const uint32_t kb = kth_key(L, lm, k_eff);
     const bool all = kb == 0u;
     if (!all || V <= kCands) {
