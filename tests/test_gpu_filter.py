@@ -151,6 +151,7 @@ def test_sampling_probs_dense_bin(n_band, by):
 @pytest.mark.parametrize("dt,V,T,top_k,top_p", [
     ("bf16", 32000, 0.6, 20, 0.95), ("fp16", 999, 1.0, 0, 0.5), ("fp32", 2048, 1.0, 0, 1.0),
     ("bf16", 5000, 0.8, 700, 0.0),
+    ("bf16", 128256, 1.0, 0, 0.95),   # whole-row draws from tile sums, no draft
 ])
 def test_sample_bit_exact(dt, V, T, top_k, top_p):
     say(f"sample {dt} V={V} T={T} top_k={top_k} top_p={top_p}")
