@@ -266,3 +266,53 @@ def test_randomized_large_thresholds():
             got.cpu().numpy().reshape(ref.shape).view(np.int32), ref.view(np.int32),
             err_msg=f"case {case}: {dt} V={V} T={T} top_k={top_k} top_p={top_p} sigma={sigma} "
                     f"kind={kind}")
+
+
+def test_randomized_filter_mix():
+    """200 random cases over every filter setting class (top_k 0/1/small/at and above 64,
+    1024, 1025, V-1, V; top_p 0 .. 1), temperatures 0.2-3, one-hot and logit drafts,
+    vocabularies 17-128256 and five row shapes: plain N(0, sigma), quantised (ties), a
+    dense band, -inf padding, one dominant token.  Chain outputs and the filtered
+    probabilities bit-exact against the oracle."""
+    say("filtered chain + get_sampling_probs: 200 randomized mixed cases")
+    rng = np.random.default_rng(606)
+    for case in range(200):
+        dt = ["bf16", "fp16", "fp32"][int(rng.integers(3))]
+        onehot = bool(rng.random() < 0.3)
+        B, k = int(rng.integers(1, 6)), int(rng.integers(0, 5))
+        V = int(rng.choice([17, 300, 1025, 4099, 20000, 50001, 128256]))
+        T = float(rng.choice([0.2, 0.7, 1.0, 1.5, 3.0]))
+        top_k = int(rng.choice([0, 1, 5, 20, 64, 65, 200, 1024, 1025, 3000, V - 1, V]))
+        top_p = float(rng.choice([0.0, 0.1, 0.5, 0.9, 0.95, 0.999, 1.0]))
+        sigma = float(rng.choice([0.1, 1.0, 2.0, 5.0]))
+        kind = str(rng.choice(["plain", "quant", "band", "pad", "peak"]))
+        g = torch.Generator().manual_seed(int(rng.integers(1 << 30)))
+        t = torch.randn((B, k + 1, V), generator=g) * sigma
+        d = t[:, :k] + torch.randn((B, k, V), generator=g) * 0.5
+        if kind == "quant":
+            t, d = torch.round(t * 2) / 2, torch.round(d * 2) / 2
+        elif kind == "band" and V > 100:
+            idx = torch.randperm(V, generator=g)[:V // 5]
+            t[..., idx] = 1.0 + 0.01 * torch.rand((B, k + 1, V // 5), generator=g)
+        elif kind == "pad" and V > 20:
+            t[..., -(V // 7):] = -float("inf")
+            d[..., -(V // 7):] = -float("inf")
+        elif kind == "peak":
+            t[..., 0] += 12.0
+            d[..., 0] += 12.0
+        t, d = t.to(DT[dt]), d.to(DT[dt])
+        ids = torch.randint(0, V, (B, k), generator=g)
+        u = torch.rand((B, k + 1), generator=g)
+        msg = (f"case {case}: {dt} onehot={onehot} B={B} k={k} V={V} T={T} top_k={top_k} "
+               f"top_p={top_p} sigma={sigma} kind={kind}")
+        ref = OAc.chain_filtered(None if onehot else d.float().numpy(), ids.numpy(),
+                                 t.float().numpy(), T, top_k, top_p, u.numpy())
+        got = S.chain_speculative_sampling_from_logits(None if onehot else d.to(DEV), ids.to(DEV),
+                                                       t.to(DEV), T, uniforms=u.to(DEV),
+                                                       top_k=top_k, top_p=top_p)
+        for a, r in zip(got, ref):
+            np.testing.assert_array_equal(a.cpu().numpy(), r, err_msg=msg)
+        pr = S.get_sampling_probs(t.to(DEV), top_p=top_p, top_k=top_k, temperature=T)
+        pref = OAc.filtered_probs(t.float().reshape(-1, V).numpy(), T, top_k, top_p)
+        np.testing.assert_array_equal(pr.cpu().numpy().reshape(pref.shape).view(np.int32),
+                                      pref.view(np.int32), err_msg=msg)
