@@ -63,7 +63,6 @@ struct ChainArgs {
   int B, k;
   int64_t V;
   float* lanes;  // [B, 2048]
-  float* gsum;   // [B, G]
   int32_t* dec;  // [B, 2]: the residual kernel's decision (j, independent accepts)
   int32_t* out_ids;
   int32_t* accepted;
@@ -239,8 +238,17 @@ struct Chain {
     return n;
   }
 
-  // Lane lam = 8*tt + ii of row j: group sums (stored) and lane sum.  Groups are
-  // computed NB at a time (their loads issued together), summed in canonical order.
+  // Sum of a group's residual values, left to right from 0 (canonical).
+  __device__ __forceinline__ static float group_sum(const float (&r)[8], int n) {
+    float gs = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < n) gs = gs + r[e];
+    return gs;
+  }
+
+  // Lane lam = 8*tt + ii of row j: its group sums and the lane sum.  Groups are computed
+  // NB at a time (their loads issued together), summed in canonical order.
   __device__ __forceinline__ float lane_sum(int b, int j, int lam, bool fallback) const {
     constexpr int NB = 4;
     const int64_t G = ceil_div(a.V, kGroup);
@@ -259,12 +267,7 @@ struct Chain {
       for (int u = 0; u < NB; ++u) {
         const int64_t g = g0 + (int64_t)u * kLanes;
         if (g < G) {
-          float gs = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (e < n[u]) gs = gs + r[u][e];
-          a.gsum[(int64_t)b * G + g] = gs;
-          s = s + gs;
+          s = s + group_sum(r[u], n[u]);
         }
       }
     }
@@ -292,7 +295,9 @@ __global__ void __launch_bounds__(256) residual_kernel(ChainArgs a) {
 template <int DT, bool LOGITS>
 __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
   __shared__ float tree[2 * kLanes];  // level 0 at [0, 2048), level l at [base_l, ...)
-  __shared__ int s_choice;
+  __shared__ float gs_lane[256];
+  __shared__ int s_choice, s_lane;
+  __shared__ float s_tg;
   Chain<DT, LOGITS> ch(a);
   const int b = blockIdx.x;
   const int t = threadIdx.x;
@@ -351,25 +356,32 @@ __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
         idx = 2 * idx + 1;
       }
     }
-    // lane idx: groups in order, then elements
-    const int tt = idx >> 3, ii = idx & 7;
-    const float* gs = a.gsum + (int64_t)b * G;
-    float cacc = 0.f, c_at = 0.f;
-    int64_t chosen = -1, last_pos = -1;
-    float c_last = 0.f;
-    // the lane's group sums, 16 loaded together, scanned in order
-    constexpr int NB = 16;
-    for (int64_t g0 = (int64_t)tt + 256 * ii; g0 < G && chosen < 0; g0 += (int64_t)NB * kLanes) {
-      float v[NB];
-#pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const int64_t g = g0 + (int64_t)u * kLanes;
-        v[u] = gs[g < G ? g : g0];
-      }
-      for (int u = 0; u < NB; ++u) {
-        const int64_t g = g0 + (int64_t)u * kLanes;
-        if (g >= G) break;
-        const float gsv = v[u];
+    s_lane = idx;
+    s_tg = tg;
+  }
+  __syncthreads();
+  // The lane's groups g = tt + 256 ii + 2048 m in order: their sums computed again, one
+  // group per thread (the residual kernel keeps none), then scanned by thread 0.
+  const int lane = s_lane;
+  const float tg = s_tg;
+  const int tt = lane >> 3, ii = lane & 7;
+  const auto rr = ch.residual_row(b, j, fallback);
+  const int64_t g_first = (int64_t)tt + 256 * ii;
+  const int64_t n_groups = g_first < G ? ceil_div(G - g_first, (int64_t)kLanes) : 0;
+  float cacc = 0.f, c_at = 0.f, c_last = 0.f;
+  int64_t chosen = -1, last_pos = -1;
+  for (int64_t m0 = 0; m0 < n_groups; m0 += 256) {
+    if (m0 + t < n_groups) {
+      float r[8];
+      const int n = ch.residual_group(rr, g_first + (m0 + t) * kLanes, r);
+      gs_lane[t] = Chain<DT, LOGITS>::group_sum(r, n);
+    }
+    __syncthreads();
+    if (t == 0 && chosen < 0) {
+      const int cnt = (int)min<int64_t>(256, n_groups - m0);
+      for (int q = 0; q < cnt; ++q) {
+        const int64_t g = g_first + (m0 + q) * kLanes;
+        const float gsv = gs_lane[q];
         const float cn = cacc + gsv;
         if (gsv > 0.f) {
           last_pos = g;
@@ -383,6 +395,9 @@ __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
         cacc = cn;
       }
     }
+    __syncthreads();
+  }
+  if (t == 0) {
     if (chosen < 0) {
       chosen = last_pos;
       c_at = c_last;
@@ -866,18 +881,18 @@ extern "C" int bsx_accept_greedy_noalloc(const int64_t* draft_d, const int64_t* 
 }
 
 static int64_t chain_ws_layout(int B, int k, int64_t V, bool logits, int64_t* off_lanes,
-                               int64_t* off_gsum, int64_t* off_dec) {
+                               int64_t* off_dec) {
+  (void)V;
   const int64_t rows = (int64_t)B * (2 * k + 1);
   const int64_t stats = logits ? acc::align256(rows * 8) : 0;
   *off_lanes = stats;
-  *off_gsum = stats + acc::align256((int64_t)B * canon::kLanes * 4);
-  *off_dec = *off_gsum + acc::align256((int64_t)B * ceil_div(V, canon::kGroup) * 4);
+  *off_dec = stats + acc::align256((int64_t)B * canon::kLanes * 4);
   return *off_dec + acc::align256((int64_t)B * 8);
 }
 
 extern "C" int64_t bsx_chain_ws_bytes(int B, int k, int64_t vocab) {
-  int64_t a, b, c;
-  return chain_ws_layout(B, k, vocab, true, &a, &b, &c);
+  int64_t a, b;
+  return chain_ws_layout(B, k, vocab, true, &a, &b);
 }
 
 template <int DT, bool LOGITS>
@@ -911,8 +926,8 @@ extern "C" int bsx_chain_speculative_sampling(const float* draft_probs_d,
   int rc = check_chain_common(draft_ids_d, uniforms_d, B, k, vocab, out_ids_d, accepted_d, emitted_d);
   if (rc != BSX_OK || B == 0) return rc;
   BSX_REQUIRE(target_probs_d, BSX_ERR_INVALID, "null target_probs");
-  int64_t off_lanes, off_gsum, off_dec;
-  const int64_t need = chain_ws_layout(B, k, vocab, false, &off_lanes, &off_gsum, &off_dec);
+  int64_t off_lanes, off_dec;
+  const int64_t need = chain_ws_layout(B, k, vocab, false, &off_lanes, &off_dec);
   BSX_REQUIRE(ws_d && ws_bytes >= need, BSX_ERR_CAPACITY, "chain workspace too small (%lld < %lld)",
               (long long)ws_bytes, (long long)need);
   acc::ChainArgs a{};
@@ -924,7 +939,6 @@ extern "C" int bsx_chain_speculative_sampling(const float* draft_probs_d,
   a.k = k;
   a.V = vocab;
   a.lanes = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_lanes);
-  a.gsum = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_gsum);
   a.dec = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) + off_dec);
   a.out_ids = out_ids_d;
   a.accepted = accepted_d;
@@ -956,8 +970,8 @@ extern "C" int bsx_chain_speculative_sampling_logits(const void* draft_logits_d,
   BSX_REQUIRE(target_logits_d, BSX_ERR_INVALID, "null target_logits");
   BSX_REQUIRE(temperature > 0.f && temperature == temperature, BSX_ERR_INVALID,
               "temperature must be > 0 (greedy acceptance has its own entry point)");
-  int64_t off_lanes, off_gsum, off_dec;
-  const int64_t need = chain_ws_layout(B, k, vocab, true, &off_lanes, &off_gsum, &off_dec);
+  int64_t off_lanes, off_dec;
+  const int64_t need = chain_ws_layout(B, k, vocab, true, &off_lanes, &off_dec);
   BSX_REQUIRE(ws_d && ws_bytes >= need, BSX_ERR_CAPACITY, "chain workspace too small (%lld < %lld)",
               (long long)ws_bytes, (long long)need);
   acc::ChainArgs a{};
@@ -971,7 +985,6 @@ extern "C" int bsx_chain_speculative_sampling_logits(const void* draft_logits_d,
   a.k = k;
   a.V = vocab;
   a.lanes = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_lanes);
-  a.gsum = reinterpret_cast<float*>(static_cast<char*>(ws_d) + off_gsum);
   a.dec = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) + off_dec);
   a.out_ids = out_ids_d;
   a.accepted = accepted_d;
