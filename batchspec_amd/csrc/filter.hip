@@ -215,8 +215,10 @@ __device__ __forceinline__ uint32_t wave_suffix_u32(uint32_t v) {
 }
 
 // Bin (11-bit key prefix) holding the k-th largest of the 2048 values lm (8 per
-// thread); -1 if k > 2048.  L.above receives the number of values in higher bins.
-// Every thread of the workgroup calls it.
+// thread); -1 if k > 2048 or if that value is -inf or NaN (those are not counted: a
+// list of candidates padded with -inf would otherwise pile its atomics onto one bin).
+// L.above receives the number of values in higher bins.  Every thread of the workgroup
+// calls it.
 __device__ __forceinline__ int kth_bin(RowsLds& L, const float (&lm)[8], int k) {
   constexpr int PER = kBins / kThreads;  // bins summed per thread
   const int t = threadIdx.x;
@@ -225,7 +227,10 @@ __device__ __forceinline__ int kth_bin(RowsLds& L, const float (&lm)[8], int k) 
   for (int i = 0; i < PER / 4; ++i) h4[t * (PER / 4) + i] = u32x4{0u, 0u, 0u, 0u};
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 8; ++i) atomicAdd(&L.hist[okey(lm[i]) >> kBinShift], 1u);
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t bin = okey(lm[i]) >> kBinShift;
+    if (bin >= (uint32_t)kFirstFiniteBin) atomicAdd(&L.hist[bin], 1u);
+  }
   __syncthreads();
   {
     uint32_t ps = 0;
@@ -301,7 +306,8 @@ __device__ __forceinline__ uint32_t kth_key(RowsLds& L, const float (&lm)[8], in
   return result;
 }
 
-// kth_key as a call: for the statistics pass's first round, where inlining it would raise
+// kth_key as a call: for the statistics pass's first round and the list tightening, where
+// inlining it would raise
 // the pass's registers (and with them the rows a compute unit holds).  The values go by
 // value, in registers (an array by reference would go through scratch memory).
 __device__ __noinline__ uint32_t kth_key_call(RowsLds& L, float v0, float v1, float v2, float v3,
@@ -938,25 +944,31 @@ __global__ void __launch_bounds__(kThreads) filter_rows_kernel(RowsArgs a) {
     __syncthreads();
   }
 
-  if (col.on && use_k && L.count > kThreads && L.count <= kCands) {
-    // With top-k on, t* is also at or above the k-th largest of the final lane maxima
-    // (each lane's maximum is at least that of its first group, so this bound is at or
-    // above the first one and the list stays complete above it): keep only those.
-    const uint32_t kb = kth_key(L, lm, k_eff);
+  if (col.on && use_k && L.count > 2 * k_eff && L.count <= kCands) {
+    // With top-k on, t* is at or above the k-th largest listed key: every element of the
+    // row at or above the bound is listed, so that is the row's k-th largest.  Keeping only
+    // the keys at or above it leaves the walk about top_k of them.
+    constexpr int PER = kCands / kThreads;
+    static_assert(PER <= 8, "the k-th selection takes 8 values per thread");
     const int n = L.count;
-    uint32_t ck[kCands / kThreads];
-    int32_t ci[kCands / kThreads];
+    uint32_t ck[PER];
+    int32_t ci[PER];
+    float cv[8];
 #pragma unroll
-    for (int j = 0; j < kCands / kThreads; ++j) {
+    for (int j = 0; j < 8; ++j) cv[j] = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
       const int s = t + kThreads * j;
       ck[j] = s < n ? L.ckey[s] : 0u;
       ci[j] = s < n ? L.cidx[s] : 0;
+      if (s < n) cv[j] = key_value(ck[j]);
     }
-    __syncthreads();
+    const uint32_t kb = kth_key_call(L, cv[0], cv[1], cv[2], cv[3], cv[4], cv[5], cv[6], cv[7],
+                                     k_eff);  // 0 (keep all) with fewer than k finite
     if (t == 0) L.count = 0;
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kCands / kThreads; ++j)
+    for (int j = 0; j < PER; ++j)
       if (t + kThreads * j < n && ck[j] >= kb) {
         const int slot = atomicAdd(&L.count, 1);
         L.ckey[slot] = ck[j];
