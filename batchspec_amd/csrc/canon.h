@@ -20,15 +20,16 @@
 //       - a lane sum adds its group sums in increasing j starting from 0;
 //       - the row sum is the balanced binary tree over the 2048 lane sums
 //         (node = left child + right child).
-//   * softmax statistics use the same lanes with an online maximum.  A lane keeps
-//     its running max m and the reference rho(m) = fl(m·C), C = log2(e) * (1/T);
-//     its elements are weighted 2^fma(x, C, -rho(m)), with rho(-inf) taken as 0 (a
-//     lane that has only seen -inf so far weighs its -inf elements 2^-inf = 0).  When
-//     a group max gm exceeds m: s *= 2^(rho(m) - rho(gm)) and m = gm; then s += the
-//     group sum of weights.
+//   * softmax statistics use the same lanes.  C = log2(e) * (1/T).  A lane keeps its
+//     running max m, its sum s and an integer-valued reference r, which starts at
+//     R0 = -2^127 (below fl(x·C) of every admissible x).  For each group, with group
+//     max gm: r' = max(r, ceil(fl(gm·C))); s = ldexp(s, sat(r - r')) (sat: conversion
+//     to int32, saturated; an exact power-of-two rescale, 0 for a lane that has only
+//     seen -inf); r = r'; m = max(m, gm); then s += the group sum of the weights
+//     2^fma(x, C, -r).
 //     The row max M is the max over lanes; the row sum Z is the binary tree over
-//     lanes of s_lane·2^(rho(m_lane) - rho(M)) (each lane rescaled exactly once).
-//     Later weights are 2^fma(x, C, -rho(M)).
+//     lanes of s_lane·2^(r_lane - rho(M)), rho(M) = fl(M·C) (each lane rescaled
+//     exactly once).  Later weights are 2^fma(x, C, -rho(M)).
 // Inputs are finite or -inf (a row needs at least one finite logit), with |x * C| below
 // 2^127 for finite x.
 #pragma once
@@ -103,31 +104,57 @@ BSX_HD float scale_for_temperature(float temperature) {
 // Weight of a logit relative to the row max: 2^(fma(x, C, -(M*C))).
 BSX_HD float weight(float x, float c, float neg_mc) { return exp2(fmaf(x, c, neg_mc)); }
 
-// -rho(m) of a lane's running max m: -(m*C), and 0 while m is -inf.
-BSX_HD float neg_ref(float m, float c) { return m == -INFINITY ? 0.0f : -(m * c); }
+// Maximum of two non-NaN floats (on the device without the NaN-quieting of fmaxf).
+BSX_HD float max_nn(float a, float b) {
+#ifdef __HIP_DEVICE_COMPILE__
+  return __builtin_elementwise_maximum(a, b);
+#else
+  return fmaxf(a, b);
+#endif
+}
 
-// Online lane state: running max m (reference rho = m*C) and weight sum s.
+// Conversion to int32 toward zero, saturated at the int32 range (-inf: INT32_MIN).
+BSX_HD int sat_i32(float v) {
+#ifdef __HIP_DEVICE_COMPILE__
+  int n;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(n) : "v"(v));
+  return n;
+#else
+  if (v != v) return 0;
+  return v <= -0x1p31f ? INT32_MIN : (v >= 0x1p31f ? INT32_MAX : (int)v);
+#endif
+}
+
+// Start value of a lane's reference: below fl(x*C) of every admissible finite x.
+constexpr float kRefStart = -0x1p127f;
+
+// Online lane state: running max m, weight sum s, integer-valued reference r.
 struct LaneState {
   float m;
   float s;
+  float r;
 };
+
+// Reference update for a group with maximum gm: returns the new reference and rescales
+// the lane sum by the exact power of two between the two references.
+BSX_HD float lane_reference(LaneState& st, float gm, float c) {
+  const float r = max_nn(st.r, ceilf(gm * c));
+  st.s = ldexpf(st.s, sat_i32(st.r - r));
+  st.r = r;
+  st.m = max_nn(st.m, gm);
+  return r;
+}
 
 // Fold one group (n elements, group max gm) into a lane.
 BSX_HD void lane_update(LaneState& st, const float* x, int n, float gm, float c) {
-  if (gm > st.m) {
-    st.s = st.s * exp2(st.m * c - gm * c);
-    st.m = gm;
-  }
-  const float neg_rho = neg_ref(st.m, c);
+  const float r = lane_reference(st, gm, c);
   float gs = 0.f;
-  for (int e = 0; e < n; ++e) gs = gs + weight(x[e], c, neg_rho);
+  for (int e = 0; e < n; ++e) gs = gs + weight(x[e], c, -r);
   st.s = st.s + gs;
 }
 
 // A lane's sum expressed relative to the row max M (rho_m = M*C).
-BSX_HD float lane_rescaled(LaneState st, float c, float rho_m) {
-  return st.s * exp2(st.m * c - rho_m);
-}
+BSX_HD float lane_rescaled(LaneState st, float rho_m) { return st.s * exp2(st.r - rho_m); }
 
 // ---- top-k / top-p filtering and fixed-point draws ----------------------------
 // Order-preserving 32-bit image of a finite float (-0 maps like +0).

@@ -82,12 +82,13 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
   for (int i = 0; i < 8; ++i) {
     st[i].m = -INFINITY;
     st[i].s = 0.f;
+    st[i].r = canon::kRefStart;
   }
   int64_t c0 = 0;
   if (vec) {
     // Whole rounds: the 8 groups t + 256*(c0 + i), i < 8, all exist and are complete.
-    // Their loads go out together; a new lane maximum (rare after the first rounds) is
-    // found with one ballot for the 8 lanes; then every weight, in the canonical order.
+    // Their loads go out together; then each lane's reference update (branch-free: an
+    // exact power-of-two rescale) and its weights, in the canonical order.
     const int64_t G_whole = V / kGroup;
     constexpr int VW = DT == BSX_DTYPE_FP32 ? 2 : 1;
     auto whole_round = [&](int64_t c0, auto first_tag) {
@@ -100,7 +101,6 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
           w[i][h] = __builtin_nontemporal_load(
               reinterpret_cast<const u32x4*>(row) + ((int64_t)t + 256 * (c0 + i)) * VW + h);
       float x[8][8], gm[8];
-      bool need = false;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if constexpr (DT == BSX_DTYPE_FP32) {
@@ -121,27 +121,18 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
                                           __builtin_elementwise_maximum(x[i][2], x[i][3])),
             __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[i][4], x[i][5]),
                                           __builtin_elementwise_maximum(x[i][6], x[i][7])));
-        need |= gm[i] > st[i].m;
       }
       if constexpr (HOOKED) {
         if constexpr (FIRST) hook->first(gm);
         hook->round(c0, gm);
       }
-      if (__builtin_amdgcn_ballot_w64(need) != 0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (gm[i] > st[i].m) {
-            st[i].s = st[i].s * canon::exp2(st[i].m * c - gm[i] * c);
-            st[i].m = gm[i];
-          }
-      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float neg_rho = canon::neg_ref(st[i].m, c);
+        const float r = canon::lane_reference(st[i], gm[i], c);
         // = 0 + w0 + ... exactly: weights are >= +0
-        float gs = canon::weight(x[i][0], c, neg_rho);
+        float gs = canon::weight(x[i][0], c, -r);
 #pragma unroll
-        for (int e = 1; e < 8; ++e) gs = gs + canon::weight(x[i][e], c, neg_rho);
+        for (int e = 1; e < 8; ++e) gs = gs + canon::weight(x[i][e], c, -r);
         st[i].s = st[i].s + gs;
       }
     };
@@ -193,7 +184,7 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
   // lanes 8t+i rescaled once, then the tree over i, over t in the wave, over waves
   float r[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = canon::lane_rescaled(st[i], c, rho_m);
+  for (int i = 0; i < 8; ++i) r[i] = canon::lane_rescaled(st[i], rho_m);
   float s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) s = s + __shfl_xor(s, m);

@@ -20,9 +20,10 @@
  *            relative error (binary32 coefficients below); ldexp(P, n).
  *   weights: w(x) = exp2(fma(x, C, -(M*C))), C = log2(e) * (1/T).
  *   groups of 8 consecutive elements; lane (8t+i) owns groups t + 256*i + 2048*j.
- *   row stats: per lane, running max m with reference fl(m*C) (0 while m = -inf;
- *   rescale on a new max), then every lane rescaled once to the row max and summed by
- *   the tree over lanes.
+ *   row stats: per lane, running max m and an integer-valued reference r (start
+ *   -2^127; per group r' = max(r, ceil(fl(gm*C))), the lane sum rescaled by
+ *   ldexp(s, sat_int32(r - r'))), weights 2^fma(x, C, -r); then every lane rescaled
+ *   once to the row max, s * exp2(r - fl(M*C)), and summed by the tree over lanes.
  *   sums: group sums left to right, lane sums over groups in j order, balanced tree
  *   over lanes; draws walk down that tree.
  * Build: cc -O2 -ffp-contract=off -fPIC -shared (see oracle/build.py).
@@ -71,41 +72,48 @@ static float tree_sum(float* v) {
   return v[0];
 }
 
-/* (M, Z) of one row of V values: per lane a running max m with reference fl(m*C);
- * weights 2^fma(x, C, -fl(m*C)); on a new max s *= 2^(fl(m*C) - fl(gm*C)).
- * M = max over lanes, Z = tree over lanes of s * 2^(fl(m*C) - fl(M*C)). */
+/* Conversion toward zero, saturated at the int32 range (-inf: INT32_MIN). */
+static int sat_i32(float v) {
+  if (v != v) return 0;
+  return v <= -0x1p31f ? INT32_MIN : (v >= 0x1p31f ? INT32_MAX : (int)v);
+}
+
+/* (M, Z) of one row of V values: per lane a running max m, a sum s and an
+ * integer-valued reference r (start -2^127, below fl(x*C) of every admissible x);
+ * per group r' = max(r, ceil(fl(gm*C))), s = ldexp(s, sat(r - r')), r = r', then the
+ * weights 2^fma(x, C, -r) summed in.  M = max over lanes, Z = tree over lanes of
+ * s * 2^(r - fl(M*C)). */
 void oc_row_stats(const float* x, int64_t V, float c, float* M, float* Z) {
   const int64_t G = ngroups(V);
-  float* lm = (float*)malloc(sizeof(float) * NL);
+  float* lr = (float*)malloc(sizeof(float) * NL);
   float* ls = (float*)malloc(sizeof(float) * NL);
   float mx = -INFINITY;
   for (int lam = 0; lam < NL; ++lam) {
-    float m = -INFINITY, s = 0.0f;
+    float m = -INFINITY, s = 0.0f, r = -0x1p127f;
     for (int64_t g = lane_first_group(lam); g < G; g += NL) {
       int64_t v0 = g * NGROUP;
       int n = (int)((V - v0) < NGROUP ? (V - v0) : NGROUP);
       float gm = x[v0];
       for (int e = 1; e < n; ++e)
         if (x[v0 + e] > gm) gm = x[v0 + e];
-      if (gm > m) {
-        s = s * oc_exp2(m * c - gm * c);
-        m = gm;
-      }
-      float neg = m == -INFINITY ? 0.0f : -(m * c);
+      const float rn = fmaxf(r, ceilf(gm * c));
+      s = ldexpf(s, sat_i32(r - rn));
+      r = rn;
+      if (gm > m) m = gm;
       float gs = 0.0f;
-      for (int e = 0; e < n; ++e) gs = gs + weight(x[v0 + e], c, neg);
+      for (int e = 0; e < n; ++e) gs = gs + weight(x[v0 + e], c, -r);
       s = s + gs;
     }
-    lm[lam] = m;
+    lr[lam] = r;
     ls[lam] = s;
     if (m > mx) mx = m;
   }
   const float rho = mx * c;
-  for (int lam = 0; lam < NL; ++lam) ls[lam] = ls[lam] * oc_exp2(lm[lam] * c - rho);
+  for (int lam = 0; lam < NL; ++lam) ls[lam] = ls[lam] * oc_exp2(lr[lam] - rho);
   *M = mx;
   *Z = tree_sum(ls);
   free(ls);
-  free(lm);
+  free(lr);
 }
 
 void oc_softmax(const float* logits, int64_t rows, int64_t V, float T, float* probs) {
