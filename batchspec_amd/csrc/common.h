@@ -54,6 +54,18 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Buffer descriptor of `bytes` bytes from `base` (below 2^31): raw 32-bit data, no
+// stride; a load at or past `bytes` returns 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000 /* data format: 32 bits */);
+}
+// Non-temporal 16-byte load at voffset (per thread) + soffset (wave-uniform) bytes.
+__device__ __forceinline__ u32x4 load_nt_b128(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset,
+                                                                         2 /* nt */));
+}
+
 // 16-bit float element -> fp32 (exact) for the two storage dtypes.
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);

@@ -91,6 +91,10 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
     // exact power-of-two rescale) and its weights, in the canonical order.
     const int64_t G_whole = V / kGroup;
     constexpr int VW = DT == BSX_DTYPE_FP32 ? 2 : 1;
+    // Buffer loads: the row's base in a descriptor, the thread's offset in a register and
+    // the group's offset in a scalar register, so no vector instruction computes an
+    // address (and a load past the row's bytes returns 0).
+    const __amdgpu_buffer_rsrc_t rsrc = row_rsrc(row, V * (int64_t)(VW == 2 ? 4 : 2));
     auto whole_round = [&](int64_t c0, auto first_tag) {
       constexpr bool FIRST = decltype(first_tag)::value;
       u32x4 w[8][VW];
@@ -98,8 +102,7 @@ __device__ void row_stats(const void* row, int64_t V, bool vec, float c, float* 
       for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int h = 0; h < VW; ++h)
-          w[i][h] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4*>(row) + ((int64_t)t + 256 * (c0 + i)) * VW + h);
+          w[i][h] = load_nt_b128(rsrc, (t * VW + h) * 16, (int)(c0 + i) * 4096 * VW);
       float x[8][8], gm[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
