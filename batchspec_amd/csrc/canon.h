@@ -31,7 +31,9 @@
 //     lanes of s_lane·2^(r_lane - rho(M)), rho(M) = fl(M·C) (each lane rescaled
 //     exactly once).  Later weights are 2^fma(x, C, -rho(M)).
 // Inputs are finite or -inf (a row needs at least one finite logit), with |x * C| below
-// 2^127 for finite x.
+// 2^31 for finite x: a weight's exponent is at most the rounding error of fl(x * C), so
+// below 2^31 every weight stays under 2^64.  Beyond it weights can overflow and a row's
+// Z become inf or NaN, the same on the CPU and the GPU.
 #pragma once
 
 #include <math.h>

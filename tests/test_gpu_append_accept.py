@@ -156,6 +156,30 @@ def test_softmax_bit_exact(dtype, V, T):
     np.testing.assert_array_equal(got.view(np.int32), ref.view(np.int32))
 
 
+def test_softmax_edge_rows_bit_exact():
+    # rows whose lanes start at -inf, rows that raise every lane's maximum at every group
+    # (ascending), large logits inside the domain (|x*C| < 2^31) and beyond it (Z NaN in
+    # both; NaN payloads are not compared)
+    V = 128256
+    say(f"softmax edge rows bf16 V={V}")
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn((6, V), generator=g) * 2
+    x[0, : 8 * 2048 * 3] = -float("inf")
+    x[1] = torch.sort(x[1]).values
+    x[2] = torch.sort(x[2], descending=True).values
+    x[3] = x[3] * 1e6
+    x[4] = x[4] * 1e8
+    x[5] = x[5] * 1e10
+    x = x.to(torch.bfloat16)
+    got = S.softmax(x.to(DEV), 1.0).cpu().numpy()
+    ref = OAc.softmax(x.float().numpy(), 1.0)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    np.testing.assert_array_equal(got[fin].view(np.int32), ref[fin].view(np.int32))
+    assert np.all(np.isfinite(got[:5]))
+    assert np.isnan(got[5]).all()
+
+
 @pytest.mark.parametrize("onehot", [False, True])
 @pytest.mark.parametrize("V", [1000, 32000])
 def test_chain_probs_bit_exact(onehot, V):

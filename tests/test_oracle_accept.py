@@ -50,6 +50,45 @@ def test_row_stats_sum_matches_fsum():
     assert abs(Z - math.fsum(w)) / math.fsum(w) < 2e-6
 
 
+def test_row_stats_lanes_starting_at_minus_inf():
+    # the first two rounds of groups are -inf, so every lane's reference starts from its
+    # start value and is rescaled from there (an exact power of two, applied to 0)
+    V = 40000
+    x = np.random.default_rng(3).normal(0, 2, size=V).astype(np.float32)
+    x[: 8 * 2048 * 2] = -np.inf
+    M, Z = A.row_stats(x)
+    fin = x[np.isfinite(x)].astype(np.float64)
+    assert M == fin.max()
+    c = np.float32(1 / math.log(2))
+    w = np.exp2(fin * float(c) - float(M) * float(c))
+    assert abs(Z - math.fsum(w)) / math.fsum(w) < 2e-6
+
+
+@pytest.mark.parametrize("order", ["ascending", "descending"])
+def test_row_stats_rescales_are_exact(order):
+    # ascending: every group raises its lane's maximum (a rescale per group); descending:
+    # none after the first.  Powers of two are exact, so only exp2 and the sums round.
+    x = np.sort(np.random.default_rng(4).normal(0, 4, size=60000).astype(np.float32))
+    if order == "descending":
+        x = x[::-1].copy()
+    M, Z = A.row_stats(x)
+    c = np.float32(1 / math.log(2))
+    w = np.exp2(x.astype(np.float64) * float(c) - float(M) * float(c))
+    assert M == x.max()
+    assert abs(Z - math.fsum(w)) / math.fsum(w) < 2e-6
+
+
+@pytest.mark.parametrize("scale", [1e3, 1e6, 1e8])
+def test_softmax_large_logits_within_domain(scale):
+    # |x * C| < 2^31: a weight's exponent is at most the rounding error of fl(x * C)
+    # (here up to 32), so Z stays finite and the probabilities sum to 1
+    x = (np.random.default_rng(5).normal(0, 1, size=(2, 5000)) * scale).astype(np.float32)
+    assert np.abs(x).max() * 1.4427 < 2.0 ** 31
+    p = A.softmax(x)
+    assert np.all(np.isfinite(p))
+    assert np.all(np.abs(p.sum(-1) - 1.0) < 1e-5)
+
+
 def test_masked_logits_have_zero_probability():
     x = np.array([0.0, -np.inf, 1.0, -1e30, 2.0], dtype=np.float32)
     p = A.softmax(x[None])[0]
