@@ -291,12 +291,51 @@ __global__ void __launch_bounds__(256) residual_kernel(ChainArgs a) {
   a.lanes[(int64_t)b * kLanes + lam] = ch.lane_sum(b, j, lam, false);
 }
 
+// Levels 1..11 of the canonical tree over the 2048 lane sums (v: lanes 8t .. 8t+7 of
+// thread t), each node the sum of its two children, stored at tree[4096 - (4096 >> l) + i]
+// for node i of level l (level 0 included): levels 1-3 from registers, 4-9 across the
+// wave by shuffles, 10-11 from the four wave nodes.  Every thread calls it; it ends with
+// a barrier.
+__device__ __forceinline__ void build_lane_tree(float* tree, const float (&v)[8]) {
+  const int t = threadIdx.x, lane = t & 63;
+  float a1[4], a2[2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) tree[8 * t + i] = v[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a1[i] = v[2 * i] + v[2 * i + 1];
+    tree[2048 + 4 * t + i] = a1[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    a2[i] = a1[2 * i] + a1[2 * i + 1];
+    tree[3072 + 2 * t + i] = a2[i];
+  }
+  float s = a2[0] + a2[1];
+  tree[3584 + t] = s;
+#pragma unroll
+  for (int d = 1, l = 4; d < 64; d <<= 1, ++l) {
+    const float o = __shfl_xor(s, d);
+    s = (lane & d) ? o + s : s + o;  // left child + right child
+    if ((lane & (2 * d - 1)) == 0) tree[4096 - (4096 >> l) + (t >> (l - 3))] = s;
+  }
+  __syncthreads();
+  if (t == 0) {
+    const float x0 = tree[4088] + tree[4089], x1 = tree[4090] + tree[4091];
+    tree[4092] = x0;
+    tree[4093] = x1;
+    tree[4094] = x0 + x1;
+  }
+  __syncthreads();
+}
+
 // grid B: tree over the 2048 lane sums, inverse-CDF walk, outputs.
 template <int DT, bool LOGITS>
 __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
-  __shared__ float tree[2 * kLanes];  // level 0 at [0, 2048), level l at [base_l, ...)
+  __shared__ float tree[2 * kLanes];  // level l at [4096 - (4096 >> l), ...)
   __shared__ float gs_lane[256];
-  __shared__ int s_choice, s_lane;
+  __shared__ float gv[256][8];  // the residual values of those groups
+  __shared__ int s_lane;
   __shared__ float s_tg;
   Chain<DT, LOGITS> ch(a);
   const int b = blockIdx.x;
@@ -305,50 +344,36 @@ __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
   const int nacc = a.dec[2 * b + 1];
   const int64_t G = ceil_div(a.V, kGroup);
 
-  for (int l = t; l < kLanes; l += 256) tree[l] = a.lanes[(int64_t)b * kLanes + l];
-  __syncthreads();
-  // build levels: level l has 2048>>l nodes at offset off_l = 4096 - (4096 >> l)
-  auto build = [&]() {
-    int off_prev = 0, n_prev = kLanes;
-    while (n_prev > 1) {
-      const int off = off_prev + n_prev;
-      const int n = n_prev >> 1;
-      for (int i = t; i < n; i += 256) tree[off + i] = tree[off_prev + 2 * i] + tree[off_prev + 2 * i + 1];
-      __syncthreads();
-      off_prev = off;
-      n_prev = n;
-    }
-  };
-  build();
+  // The row statistics of row j are read now, before the tree is built (the walk's
+  // group sums need them).
+  auto rr = ch.residual_row(b, j, false);
+  {
+    float v[8];
+    const float* ls = a.lanes + (int64_t)b * kLanes + 8 * t;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = ls[i];
+    build_lane_tree(tree, v);
+  }
   bool fallback = false;
   if (!(tree[2 * kLanes - 2] > 0.f)) {
     // No residual mass (p_j <= q_j everywhere in fp32): draw from p_j instead.
     fallback = true;
+    rr.with_q = false;
+    rr.dr = rr.tr;
+    rr.dvec = rr.tvec;
+    float v[8];
+    for (int w = 0; w < 8; ++w) v[w] = ch.lane_sum(b, j, 8 * t + w, true);
     __syncthreads();
-    for (int w = 0; w < 8; ++w) tree[8 * t + w] = ch.lane_sum(b, j, 8 * t + w, true);
-    __syncthreads();
-    build();
+    build_lane_tree(tree, v);
   }
   if (t == 0) {
     const float u = a.uniforms[(int64_t)b * (a.k + 1) + a.k];
-    const float total = tree[2 * kLanes - 2];
-    float tg = u * total;
-    // descend: node i at level l (offset off_l); children at level l-1: 2i, 2i+1
+    float tg = u * tree[2 * kLanes - 2];
     int idx = 0;
-    int offs[12];
-    {
-      int off = 0, n = kLanes, l = 0;
-      while (true) {
-        offs[l] = off;
-        if (n == 1) break;
-        off += n;
-        n >>= 1;
-        ++l;
-      }
-    }
     for (int l = 11; l >= 1; --l) {
-      const float left = tree[offs[l - 1] + 2 * idx];
-      const float right = tree[offs[l - 1] + 2 * idx + 1];
+      const int off = 4096 - (4096 >> (l - 1));  // level l - 1
+      const float left = tree[off + 2 * idx];
+      const float right = tree[off + 2 * idx + 1];
       if (tg < left || !(right > 0.f)) {
         idx = 2 * idx;
       } else {
@@ -361,20 +386,23 @@ __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
   }
   __syncthreads();
   // The lane's groups g = tt + 256 ii + 2048 m in order: their sums computed again, one
-  // group per thread (the residual kernel keeps none), then scanned by thread 0.
+  // group per thread (the residual kernel keeps none), then scanned by thread 0; the
+  // values of a chunk's groups stay in LDS for the element scan.
   const int lane = s_lane;
   const float tg = s_tg;
-  const int tt = lane >> 3, ii = lane & 7;
-  const auto rr = ch.residual_row(b, j, fallback);
-  const int64_t g_first = (int64_t)tt + 256 * ii;
+  const int64_t g_first = (int64_t)(lane >> 3) + 256 * (lane & 7);
   const int64_t n_groups = g_first < G ? ceil_div(G - g_first, (int64_t)kLanes) : 0;
   float cacc = 0.f, c_at = 0.f, c_last = 0.f;
   int64_t chosen = -1, last_pos = -1;
+  float rc[8];
+  int nc = 0;
   for (int64_t m0 = 0; m0 < n_groups; m0 += 256) {
     if (m0 + t < n_groups) {
       float r[8];
       const int n = ch.residual_group(rr, g_first + (m0 + t) * kLanes, r);
       gs_lane[t] = Chain<DT, LOGITS>::group_sum(r, n);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) gv[t][e] = e < n ? r[e] : 0.f;
     }
     __syncthreads();
     if (t == 0 && chosen < 0) {
@@ -390,6 +418,9 @@ __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
         if (tg < cn) {
           chosen = g;
           c_at = cacc;
+          nc = (int)min<int64_t>(kGroup, a.V - g * kGroup);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) rc[e] = gv[q][e];
           break;
         }
         cacc = cn;
@@ -398,20 +429,20 @@ __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
     __syncthreads();
   }
   if (t == 0) {
-    if (chosen < 0) {
+    if (chosen < 0 && last_pos >= 0) {
+      // the last group with mass (its values may have left LDS with a later chunk)
       chosen = last_pos;
       c_at = c_last;
+      nc = ch.residual_group(rr, chosen, rc);
     }
     int64_t tok = -1;
     if (chosen >= 0) {
       const float tl = tg - c_at;
-      float r[8];
-      const int n = ch.residual_group(ch.residual_row(b, j, fallback), chosen, r);
       float s = 0.f;
       int64_t last_e = -1;
-      for (int e = 0; e < n; ++e) {
-        s = s + r[e];
-        if (r[e] > 0.f) last_e = e;
+      for (int e = 0; e < nc; ++e) {
+        s = s + rc[e];
+        if (rc[e] > 0.f) last_e = e;
         if (tl < s) {
           tok = chosen * kGroup + e;
           break;
@@ -419,7 +450,6 @@ __global__ void __launch_bounds__(256) pick_kernel(ChainArgs a) {
       }
       if (tok < 0 && last_e >= 0) tok = chosen * kGroup + last_e;
     }
-    s_choice = (int)tok;
     int32_t* out = a.out_ids + (int64_t)b * (a.k + 1);
     for (int i = 0; i <= a.k; ++i) {
       int32_t v = -1;

@@ -213,6 +213,32 @@ def test_chain_logits_bit_exact_small(onehot, T):
         np.testing.assert_array_equal(a.cpu().numpy(), r)
 
 
+@pytest.mark.parametrize("V", [3000, 128256])
+def test_chain_logits_no_residual_mass_draws_from_target(V):
+    # draft rows equal to the target rows and every draft token at a -inf logit of both:
+    # p(x) = q(x) = 0 rejects position 0, the residual max(0, p - q) has no mass, and the
+    # emitted token is drawn from p_0 itself (the pick kernel's second tree)
+    B, k = 6, 3
+    say(f"chain logits without residual mass V={V}")
+    g = torch.Generator().manual_seed(V + 5)
+    tl = (torch.randn((B, k + 1, V), generator=g) * 2).to(torch.bfloat16)
+    ids = torch.randint(0, V, (B, k), generator=g)
+    for b in range(B):
+        for i in range(k):
+            tl[b, i, ids[b, i]] = -float("inf")
+    dl = tl[:, :k].clone()
+    u = torch.rand((B, k + 1), generator=g)
+    ref = OAc.chain_logits(dl.float().numpy(), ids.numpy(), tl.float().numpy(), 1.0, u.numpy())
+    got = S.chain_speculative_sampling_from_logits(dl.to(DEV), ids.to(DEV), tl.to(DEV), 1.0,
+                                                   uniforms=u.to(DEV))
+    for a, r in zip(got, ref):
+        np.testing.assert_array_equal(a.cpu().numpy(), r)
+    out = got[0].cpu().numpy()
+    assert (got[2].cpu().numpy() == 0).all()  # every request stops at position 0
+    for b in range(B):
+        assert 0 <= out[b, 0] < V and np.isfinite(tl[b, 0, out[b, 0]].float().item())
+
+
 def test_config5_full_size_bit_exact():
     say("config 5 full size: B=128, k=5, V=128256, bf16, T=1")
     c = stochastic_case(device=DEV)
