@@ -995,6 +995,8 @@ extern "C" int bsx_chain_speculative_sampling_logits(const void* draft_logits_d,
                                                      int32_t* out_ids_d, int32_t* accepted_d,
                                                      int32_t* emitted_d, void* ws_d,
                                                      int64_t ws_bytes, void* stream) {
+  BSX_REQUIRE(row_bytes_ok(vocab, dtype), BSX_ERR_UNSUPPORTED,
+              "a row of %lld logits is 2^31 bytes or more", (long long)vocab);
   int rc = check_chain_common(draft_ids_d, uniforms_d, B, k, vocab, out_ids_d, accepted_d, emitted_d);
   if (rc != BSX_OK || B == 0) return rc;
   BSX_REQUIRE(target_logits_d, BSX_ERR_INVALID, "null target_logits");
@@ -1048,6 +1050,8 @@ extern "C" int bsx_softmax(const void* logits_d, int dtype, float temperature, i
                            int64_t vocab, float* probs_d, void* ws_d, int64_t ws_bytes,
                            void* stream) {
   BSX_REQUIRE(rows >= 0 && vocab > 0, BSX_ERR_INVALID, "bad shape");
+  BSX_REQUIRE(row_bytes_ok(vocab, dtype), BSX_ERR_UNSUPPORTED,
+              "a row of %lld logits is 2^31 bytes or more", (long long)vocab);
   if (rows == 0) return BSX_OK;
   BSX_REQUIRE(logits_d && probs_d && ws_d, BSX_ERR_INVALID, "null pointer");
   BSX_REQUIRE(temperature > 0.f, BSX_ERR_INVALID, "temperature must be > 0");

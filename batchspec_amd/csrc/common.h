@@ -54,6 +54,12 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Rows read through buffer descriptors are addressed with 32-bit byte offsets: a row of
+// logits must stay below 2^31 bytes (entry points reject larger ones).
+inline bool row_bytes_ok(int64_t vocab, int dtype) {
+  return vocab > 0 && vocab * (dtype == BSX_DTYPE_FP32 ? 4 : 2) < (1LL << 31);
+}
+
 // Buffer descriptor of `bytes` bytes from `base` (below 2^31): raw 32-bit data, no
 // stride; a load at or past `bytes` returns 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, int64_t bytes) {

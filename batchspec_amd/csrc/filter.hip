@@ -1519,6 +1519,8 @@ extern "C" int bsx_chain_speculative_sampling_filtered(
     int dtype, float temperature, int top_k, float top_p, const float* uniforms_d, int B, int k,
     int64_t vocab, int32_t* out_ids_d, int32_t* accepted_d, int32_t* emitted_d, void* ws_d,
     int64_t ws_bytes, void* stream) {
+  BSX_REQUIRE(row_bytes_ok(vocab, dtype), BSX_ERR_UNSUPPORTED,
+              "a row of %lld logits is 2^31 bytes or more", (long long)vocab);
   if (!filters_on(top_k, top_p, vocab))
     return bsx_chain_speculative_sampling_logits(draft_logits_d, draft_ids_d, target_logits_d,
                                                  dtype, temperature, uniforms_d, B, k, vocab,
@@ -1572,6 +1574,8 @@ extern "C" int64_t bsx_sample_ws_bytes(int64_t rows, int64_t vocab) {
 extern "C" int bsx_sample(const void* logits_d, int dtype, float temperature, int top_k,
                           float top_p, const float* uniforms_d, int64_t rows, int64_t vocab,
                           int32_t* out_d, void* ws_d, int64_t ws_bytes, void* stream) {
+  BSX_REQUIRE(row_bytes_ok(vocab, dtype), BSX_ERR_UNSUPPORTED,
+              "a row of %lld logits is 2^31 bytes or more", (long long)vocab);
   BSX_REQUIRE(rows >= 0 && rows < (1LL << 31) && vocab > 0, BSX_ERR_INVALID, "bad shape");
   if (rows == 0) return BSX_OK;
   BSX_REQUIRE(logits_d && uniforms_d && out_d && ws_d, BSX_ERR_INVALID, "null pointer");
@@ -1608,6 +1612,8 @@ static int sampling_probs_impl(const void* logits, int64_t rows, int64_t V, floa
 extern "C" int bsx_sampling_probs(const void* logits_d, int dtype, float temperature, int top_k,
                                   float top_p, int64_t rows, int64_t vocab, float* probs_d,
                                   void* ws_d, int64_t ws_bytes, void* stream) {
+  BSX_REQUIRE(row_bytes_ok(vocab, dtype), BSX_ERR_UNSUPPORTED,
+              "a row of %lld logits is 2^31 bytes or more", (long long)vocab);
   if (!filters_on(top_k, top_p, vocab))
     return bsx_softmax(logits_d, dtype, temperature, rows, vocab, probs_d, ws_d, ws_bytes, stream);
   BSX_REQUIRE(rows >= 0 && rows < (1LL << 31) && vocab > 0 && vocab < (1LL << 31),

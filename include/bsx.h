@@ -19,6 +19,8 @@
  *     thread-local message. Nothing throws across the ABI.
  *   - Integer index tensors are int32 (CSR page tables) or int64 (token ids), as
  *     in the reference.
+ *   - A row of logits (vocab x dtype size) must stay below 2^31 bytes in the softmax,
+ *     sampling and acceptance-from-logits entry points (BSX_ERR_UNSUPPORTED otherwise).
  */
 #ifndef BSX_H
 #define BSX_H

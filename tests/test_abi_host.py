@@ -33,6 +33,26 @@ def test_library_exports_every_header_symbol(bsx):
     assert bsx.bsx_version() == 1
 
 
+def test_rows_of_2_31_bytes_are_rejected_before_any_gpu_call():
+    # the row statistics read logits through buffer descriptors (32-bit byte offsets):
+    # every entry point that reaches them rejects a row of 2^31 bytes, before any HIP call
+    L = _lib.load()
+    unsupported = -3
+    V32, V16 = 1 << 29, 1 << 30  # 2^31 bytes as fp32 / as 16-bit logits
+    assert L.bsx_softmax(None, 2, 1.0, 1, V32, None, None, 0, None) == unsupported
+    assert b"2^31 bytes" in L.bsx_last_error()
+    assert L.bsx_softmax(None, 0, 1.0, 1, V16, None, None, 0, None) == unsupported
+    assert L.bsx_softmax(None, 0, 1.0, 1, V16 - 1, None, None, 0, None) == -1  # null pointers
+    assert L.bsx_chain_speculative_sampling_logits(None, None, None, 0, 1.0, None, 1, 1, V16,
+                                                   None, None, None, None, 0, None) == unsupported
+    assert L.bsx_chain_speculative_sampling_filtered(None, None, None, 0, 1.0, 20, 0.9, None, 1,
+                                                     1, V16, None, None, None, None, 0,
+                                                     None) == unsupported
+    assert L.bsx_sampling_probs(None, 0, 1.0, 20, 0.9, 1, V16, None, None, 0,
+                                None) == unsupported
+    assert L.bsx_sample(None, 0, 1.0, 20, 0.9, None, 1, V16, None, None, 0, None) == unsupported
+
+
 def _plan(qo, kvp, last, Hq=32, Hkv=8, D=128, ps=16, mode=_lib.MASK_CAUSAL, cus=256, sink=0,
           window=0, nidx=-1):
     L = _lib.load()
