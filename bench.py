@@ -363,7 +363,7 @@ def cpu_model() -> str:
 
 
 def cpu_baseline(b, runs: int = 5):
-    """The reference's CPU path as BASELINE.md defines it: torch fp32 paged gather +
+    """The reference's CPU path: torch fp32 paged gather +
     scaled_dot_product_attention (bottom-right causal bool mask, GQA) over the whole
     config-2 batch, on the host's threads; median of `runs` runs after one warmup.
     Then the C restatement of the stochastic acceptance (oracle/accept.c) over config 5,
