@@ -77,3 +77,50 @@ def test_chain_sampling_graph_replays(top_k, top_p):
                                       u.cpu().numpy())
             for a, r in zip(got, want):
                 np.testing.assert_array_equal(a, r, err_msg="replay 0 against the oracle")
+
+
+@pytest.mark.parametrize("top_k,top_p", [(20, 0.95), (0, 0.95), (2000, 0.0), (0, 1.0)])
+def test_sample_and_sampling_probs_graph_replays(top_k, top_p):
+    """sample() and get_sampling_probs (batchspec/backends/utils/sampling.py:18-115) captured
+    in one graph, replayed on new logits and uniforms written into the captured buffers;
+    each replay equals the same calls run eagerly on copies, the first also the oracle."""
+    R, Sq, V2 = 16, 1, 32000
+    say(f"sample + sampling probs in a graph: rows={R} V={V2} top_k={top_k} top_p={top_p}")
+    lg = torch.zeros((R, Sq, V2), dtype=torch.bfloat16, device=DEV)
+    uu = torch.zeros((R, Sq), dtype=torch.float32, device=DEV)
+
+    def fill(seed, sigma):
+        g = torch.Generator().manual_seed(seed)
+        lg.copy_((torch.randn((R, Sq, V2), generator=g) * sigma).to(torch.bfloat16))
+        uu.copy_(torch.rand((R, Sq), generator=g))
+
+    def step():
+        ids = S.sample(lg, top_p, top_k, 0.8, uniforms=uu)
+        probs = S.get_sampling_probs(lg, top_p, top_k, 0.8)
+        return ids, probs
+
+    fill(0, 2.0)
+    step()  # allocates the workspaces outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    torch.cuda.synchronize()
+    for rep, sigma in enumerate([2.0, 0.3, 6.0, 2.0]):
+        fill(200 + rep, sigma)
+        ref_ids = S.sample(lg.clone(), top_p, top_k, 0.8, uniforms=uu.clone()).cpu().numpy()
+        ref_p = S.get_sampling_probs(lg.clone(), top_p, top_k, 0.8).cpu().numpy()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out[0].cpu().numpy(), ref_ids, err_msg=f"ids, replay {rep}")
+        np.testing.assert_array_equal(out[1].cpu().numpy().view(np.int32), ref_p.view(np.int32),
+                                      err_msg=f"probs, replay {rep}")
+        if rep == 0:
+            x = lg.float().cpu().numpy().reshape(R * Sq, V2)
+            want = OAc.filtered_probs(x, 0.8, top_k, top_p)
+            np.testing.assert_array_equal(out[1].cpu().numpy().reshape(R * Sq, V2).view(np.int32),
+                                          want.view(np.int32), err_msg="probs against the oracle")
+            want_ids = OAc.sample(x, 0.8, top_k, top_p, uu.cpu().numpy().reshape(-1))
+            np.testing.assert_array_equal(out[0].cpu().numpy().reshape(-1), want_ids,
+                                          err_msg="ids against the oracle")
