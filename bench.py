@@ -28,7 +28,10 @@ Printed: one JSON line with
   accepted_tok_s  accepted tokens/s of a 32-layer verify step: the page-table update
               (insert + delete), one device plan, 32 x (append + attention) and the
               fused greedy acceptance over [64, 5, 128256] bf16 logits (draft = target
-              argmax with probability 0.7), reference acceptance rule
+              argmax with probability 0.7), reference acceptance rule;
+              accepted_tok_s_sampling the same step with the reference's default
+              sampling acceptance instead (sampling_accept_mtp: T=0.6, top_k=20,
+              top_p=0.95, one-hot drafts, accept = emitted + 1)
   cpu_baseline    torch fp32 paged gather + scaled_dot_product_attention over the
               config-2 batch on the host cores (median of 5 runs after 1 warmup), and
               the C acceptance restatement over config 5
@@ -232,6 +235,24 @@ def acceptance(dev, iters, out):
     out["greedy_accept"] = {"us": round(t_acc, 2), "GB/s": round(gbytes / t_acc / 1e3, 1),
                             "frac": round(gbytes / t_acc / 1e3 / HBM_PEAK_GBS, 4),
                             "bytes": gbytes, "workload": "[64, 5, 128256] bf16 logits, fused argmax"}
+    # the reference's default sampling mode (temperature 0.6, top_k 20, top_p 0.95;
+    # batchspec/args.py:104-116) as the MTP branch of evaluate_posterior runs it
+    # (mtp_engine.py:561-575: filtered target, one-hot drafts, accept = emitted + 1), on
+    # the same logits and drafts
+    gu = g.uniforms.to(dev)
+
+    def sampling_accept():
+        return bsx.sampling.chain_speculative_sampling_from_logits(
+            None, gd, gl, 0.6, uniforms=gu, top_k=20, top_p=0.95)
+
+    samp_us = time_events(lambda i: sampling_accept(), iters, 3)
+    acc_samp = sampling_accept()[2] + 1
+    t_samp = mean(samp_us)
+    out["sampling_accept_mtp"] = {
+        "us": round(t_samp, 2), "GB/s": round(gbytes / t_samp / 1e3, 1),
+        "frac": round(gbytes / t_samp / 1e3 / HBM_PEAK_GBS, 4), "bytes": gbytes,
+        "workload": "[64, 5, 128256] bf16 target logits, one-hot drafts, T=0.6, top_k=20, "
+                    "top_p=0.95"}
     del gl, g
     s = stochastic_case(device=dev)
     n = max(5, iters // 3)
@@ -262,7 +283,7 @@ def acceptance(dev, iters, out):
     out["stochastic_accept_top_p095"] = {
         "us": round(t_sp, 2), "GB/s": round(sbytes / t_sp / 1e3, 1),
         "frac": round(sbytes / t_sp / 1e3 / HBM_PEAK_GBS, 4), "bytes": sbytes}
-    return t_acc, acc_ref, acc_pre
+    return t_acc, acc_ref, acc_pre, t_samp, acc_samp
 
 
 def step_plumbing(dev, iters, sets, acc_ref):
@@ -587,7 +608,7 @@ def main() -> int:
     t_acc = None
     if not args.skip_accept:
         log("acceptance: greedy [64,5,128256], stochastic config 5")
-        t_acc, acc_ref, acc_pre = acceptance(dev, args.steps, result)
+        t_acc, acc_ref, acc_pre, t_samp, acc_samp = acceptance(dev, args.steps, result)
 
     if not args.no_extra:
         log("verify attention at configs 4, 3b, 3a")
@@ -607,11 +628,16 @@ def main() -> int:
             result["accepted_tok_s_prefix_rule"] = round(n_pre / (t_model * 1e-6), 1)
             result["accepted_tok_s_host_plan"] = round(
                 n_ref / ((t_model - t_plan + t_host) * 1e-6), 1)
-            result["mean_accept_len"] = {"reference_rule": n_ref / 64, "prefix_rule": n_pre / 64}
+            t_model_s = t_model - t_acc + t_samp
+            n_samp = int(acc_samp.sum())
+            result["accepted_tok_s_sampling"] = round(n_samp / (t_model_s * 1e-6), 1)
+            result["mean_accept_len"] = {"reference_rule": n_ref / 64, "prefix_rule": n_pre / 64,
+                                         "sampling": n_samp / 64}
             result["verify_step_us"] = {
                 "total": round(t_model, 1), "page_table": t_pt, "device_plan": t_plan,
                 "layers_attention_append": round(NUM_LAYERS * (t_attn + t_app), 1),
-                "greedy_accept": round(t_acc, 2), "layers": NUM_LAYERS}
+                "greedy_accept": round(t_acc, 2), "sampling_accept": round(t_samp, 2),
+                "layers": NUM_LAYERS}
 
     if not args.no_cpu_baseline:
         log("CPU baseline: torch fp32 SDPA over config 2, C acceptance over config 5")
