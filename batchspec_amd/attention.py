@@ -115,6 +115,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._graph_shape: Optional[_lib.AttnPlan] = None
         self._graph_static: Optional[tuple] = None
         self._captured_sig: Optional[tuple] = None
+        self._captured_rows = 0
         self._host_blob: Optional[np.ndarray] = None
 
     # ------------------------------------------------------------------ plan
@@ -217,7 +218,9 @@ class BatchPrefillWithPagedKVCacheWrapper:
             static = (int(num_qo_heads), int(num_kv_heads), int(head_dim_qk), int(page_size),
                       mode, int(sink_tokens), int(window_tokens), float(sm_scale or 0.0))
             max_qo = int(np.diff(qo_h).max()) if batch > 0 else 0
+            # the shape is adopted only once the plan passes _check_captured below
             shape = self._fixed_shape(lib, batch, max(max_qo, int(max_qo_len or 0)), static)
+            new_shape = (shape, static)
             bound = int(shape.plan_ints)
             blob = np.zeros(bound, dtype=np.int32)
             rc = lib.bsx_attn_plan_fixed(ctypes.byref(shape), qo_h.ctypes.data, kvp_h.ctypes.data,
@@ -226,6 +229,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan")
             blob_bytes = _align(bound * 4)
         else:
+            new_shape = None
             bound = int(lib.bsx_attn_plan_ints_bound(batch, self._num_cus))
             blob = np.empty(bound, dtype=np.int32)
             rc = lib.bsx_attn_plan(qo_h.ctypes.data, kvp_h.ctypes.data, last_h.ctypes.data, batch,
@@ -240,6 +244,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
             raise ValueError(f"float_workspace_buffer too small: need {need} bytes, "
                              f"have {self._ws.numel()}")
         self._check_captured(plan, blob_bytes)
+        if new_shape is not None:
+            self._graph_shape, self._graph_static = new_shape
         self._blob_bytes = blob_bytes
         self._host_blob = blob[: int(plan.plan_ints)].copy()
 
@@ -293,7 +299,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
 
     def _fixed_shape(self, lib, batch: int, max_qo: int, static: tuple) -> _lib.AttnPlan:
         """The bound-sized shape of graph mode: kept while plans fit it (same heads, page
-        size and mask; at most its requests and query tokens per request)."""
+        size and mask; at most its requests and query tokens per request).  Returns the
+        shape without adopting it: plan() adopts it once the plan is accepted."""
         shp = self._graph_shape
         if shp is not None and self._graph_static == static and batch <= shp.batch \
                 and max(max_qo, 1) <= shp.max_qo_len:
@@ -309,7 +316,6 @@ class BatchPrefillWithPagedKVCacheWrapper:
         rc = lib.bsx_attn_plan_device_shape(max(cap_b, 1), nq, nk, d, ps, mode, sink, window, scale,
                                             self._num_cus, max(max_qo, 1), ctypes.byref(new))
         _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan")
-        self._graph_shape, self._graph_static = new, static
         return new
 
     @staticmethod
@@ -318,14 +324,22 @@ class BatchPrefillWithPagedKVCacheWrapper:
                      if n not in ("total_qo", "total_tiles")) + (blob_bytes,)
 
     def _check_captured(self, plan: _lib.AttnPlan, blob_bytes: int) -> None:
-        """In graph mode a captured run() replays with the launch arguments it was
-        captured with; a plan that would need others is refused instead of being
-        replayed stale."""
-        if self._captured_sig is not None and self._launch_sig(plan, blob_bytes) != self._captured_sig:
+        """In graph mode a captured run() replays with the launch arguments and the q /
+        out / lse buffers it was captured with; a plan that would need other arguments,
+        or more query token rows than those buffers hold, is refused instead of being
+        replayed stale (or past the buffers' ends)."""
+        if self._captured_sig is None:
+            return
+        if self._launch_sig(plan, blob_bytes) != self._captured_sig:
             raise ValueError(
                 "plan(): a graph captured run() of this wrapper, and this plan needs a larger "
                 "fixed shape (more requests or query tokens per request, or other heads / mask); "
                 "pass max_qo_len= to the first plan() or use a new wrapper for the new shape")
+        if int(plan.total_qo) > self._captured_rows:
+            raise ValueError(
+                f"plan(): a graph captured run() with q / out of {self._captured_rows} token "
+                f"rows, and this plan has {int(plan.total_qo)} query tokens; capture run() with "
+                "buffers sized for the largest step")
 
     @property
     def plan_blob(self) -> Optional[np.ndarray]:
@@ -466,8 +480,11 @@ class BatchPrefillWithPagedKVCacheWrapper:
             raise ValueError("out must match q in shape and dtype with dense heads")
         if return_lse and lse is None:
             lse = torch.empty((q.shape[0], plan.num_qo_heads), dtype=torch.float32, device=dev)
-        if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()):
-            raise ValueError("lse must be a contiguous float32 tensor")
+        if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()
+                                or lse.dim() != 2 or lse.shape[1] != plan.num_qo_heads
+                                or lse.shape[0] < plan.total_qo):
+            raise ValueError(f"lse must be a contiguous float32 tensor of at least "
+                             f"[{plan.total_qo}, {plan.num_qo_heads}]")
         ws = self._ws
         blob = ws[: int(plan.plan_ints) * 4]
         fws = ws[self._blob_bytes:] if int(plan.float_ws_bytes) > 0 else None
@@ -483,6 +500,10 @@ class BatchPrefillWithPagedKVCacheWrapper:
         _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.run")
         if torch.cuda.is_current_stream_capturing():
             self._captured_sig = self._launch_sig(plan, self._blob_bytes)
+            rows = min(q.shape[0], out.shape[0])
+            if lse is not None:
+                rows = min(rows, lse.shape[0])
+            self._captured_rows = rows if self._captured_rows == 0 else min(rows, self._captured_rows)
         return (out, lse) if return_lse else out
 
     forward = run

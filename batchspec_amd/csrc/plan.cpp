@@ -412,6 +412,13 @@ extern "C" int bsx_attn_plan_fixed(const bsx_attn_plan_t* shape, const int32_t* 
   PLAN_REQUIRE(hs.nseg <= shape->num_segments, BSX_ERR_CAPACITY,
                "schedule of %d segments exceeds the fixed bound %d", hs.nseg,
                shape->num_segments);
+  // the merge-record region between off_merge_seqs and off_part_indptr holds one record
+  // per request of the shape; the partial slots are bounded by the segments above
+  PLAN_REQUIRE((int64_t)hs.merge_seqs.size() <= shape->batch &&
+                   (int64_t)hs.part_indptr[batch] <= shape->num_partials,
+               BSX_ERR_CAPACITY, "schedule of %d merge records / %d partial slots exceeds the "
+               "fixed bounds %d / %d", (int)hs.merge_seqs.size(), (int)hs.part_indptr[batch],
+               shape->batch, shape->num_partials);
   write_blob(hs, qo_indptr_h, kv_indptr_h, batch, shape->batch, W, shape->off_seq,
              shape->off_seg_indptr, shape->off_segments, shape->off_merge_seqs,
              shape->off_part_indptr, plan_blob_h);

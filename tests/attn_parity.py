@@ -96,11 +96,15 @@ def _tree_words(b, r):
     return np.asarray(b.mask_words[q0:q1], dtype=np.uint64)
 
 
-def segment_boundaries(plan_blob, plan, r, kv_len):
-    """First and last kv token of each segment of request r in a host plan's blob."""
-    if plan_blob is None:
+def segment_boundaries(plan_blob, plan, r, kv_len, segments=None):
+    """First and last kv token of each segment of request r, from a host plan's blob or
+    from a segment list [S, 4] = (request, first tile, end tile, slot)."""
+    if segments is not None:
+        segs = np.asarray(segments).reshape(-1, 4)
+    elif plan_blob is None:
         return []
-    segs = plan_blob[plan.off_segments: plan.off_segments + 4 * plan.num_segments].reshape(-1, 4)
+    else:
+        segs = plan_blob[plan.off_segments: plan.off_segments + 4 * plan.num_segments].reshape(-1, 4)
     out = []
     for b, t0, t1, _ in segs:
         if b != r or t1 <= t0:
@@ -111,9 +115,10 @@ def segment_boundaries(plan_blob, plan, r, kv_len):
 
 
 def plant_keys(b, mode="causal", plan_blob=None, plan=None, seed=0, sink=0, window=0,
-               beta=4.0, margin=1.0):
+               beta=4.0, margin=1.0, segments=None):
     """Rewrite b.q and b.cache (device tensors) in place; returns the planted targets
-    {(request, kv head, row): position} for diagnostics."""
+    {(request, kv head, row): position} for diagnostics.  Segment boundaries come from
+    a host plan (plan_blob, plan) or a segment list (segments, e.g. a device plan's)."""
     rng = np.random.default_rng(seed)
     dev = b.q.device
     Hq, Hkv, D, ps = b.num_qo_heads, b.num_kv_heads, b.head_dim, b.page_size
@@ -133,7 +138,8 @@ def plant_keys(b, mode="causal", plan_blob=None, plan=None, seed=0, sink=0, wind
         diag = L - n_q
         S = float(np.log(max(L, 2))) + margin
         gamma = S / (beta * sm)
-        bounds = [p for p in segment_boundaries(plan_blob, plan, r, L) if p < max(diag, 1)]
+        bounds = [p for p in segment_boundaries(plan_blob, plan, r, L, segments)
+                  if p < max(diag, 1)]
         words = _tree_words(b, r) if mode == "tree" else None
         for h in range(Hkv):
             tgt = []

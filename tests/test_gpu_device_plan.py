@@ -1,8 +1,11 @@
 """GPU tests of the device-side attention schedule (bsx_attn_plan_device through
 plan(on_device=True)): the blob equals the CPU restatement (oracle/attn_schedule.py)
-entry for entry, attention run on it matches the fp32 oracle within the north star's
-2e-2, a graph holding plan and run replays correctly after the page table changes,
-and a malformed table yields the error code and an empty schedule."""
+entry for entry, attention run on it matches the fp32 oracle under the checks of
+tests/attn_parity.py (the north star's elementwise 2e-2 plus the normalised bounds and
+the lse), with planted keys and guards at the benchmark shapes so a dropped mask, a
+lost last tile or an all-zeros output fails; a graph holding plan and run replays
+correctly after the page table changes, and a malformed table yields the error code
+and an empty schedule."""
 import sys
 
 import numpy as np
@@ -10,13 +13,13 @@ import pytest
 import torch
 
 import batchspec_amd as bsx
-from batchspec_amd.workloads import make_verify_batch
+from batchspec_amd.workloads import config2, make_verify_batch
 from oracle import attention as OA
 from oracle import attn_schedule as OS
+from tests import attn_parity as AP
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
-ATOL = RTOL = 2e-2
 
 
 def say(msg):
@@ -24,18 +27,17 @@ def say(msg):
     sys.stdout.flush()
 
 
-def check(got, ref):
-    g = got.float().cpu().numpy()
-    assert np.isfinite(g).all()
-    err = np.abs(g - ref) - (ATOL + RTOL * np.abs(ref))
-    assert err.max() <= 0, f"max excess {err.max():.4g}, max abs err {np.abs(g - ref).max():.4g}"
+def check(got, ref, lse_got=None, lse_ref=None):
+    """The full-size check of tests/attn_parity.py: elementwise 2e-2 + 2e-2|ref|, max
+    error within 2e-2 max|ref|, relative L2 within 1e-2, lse within 5e-3."""
+    return AP.check(got, ref, lse_got, lse_ref)
 
 
 def oracle(b, mode, **kw):
     return OA.verify_attention(b.q.float().cpu().numpy(), b.cache.float().cpu().numpy(),
                                b.qo_indptr.cpu().numpy(), b.kv_indptr.cpu().numpy(),
                                b.kv_indices.cpu().numpy(), b.kv_last_page_len.cpu().numpy(),
-                               b.page_size, mode=mode, **kw)
+                               b.page_size, mode=mode, return_lse=True, **kw)
 
 
 def wrapper(mb=256, **kw):
@@ -66,28 +68,76 @@ def compare_schedule(w, b, max_qo, mode=1, sink=0, window=0):
         np.testing.assert_array_equal(got[k], want[k], err_msg=k)
     OS.check_invariants(got, b.qo_indptr.cpu().numpy(), b.kv_indptr.cpu().numpy(),
                         b.kv_last_page_len.cpu().numpy(), b.page_size, mode, sink, window)
+    return got
 
 
-@pytest.mark.parametrize("B,lo,hi,qo,hq,hkv,d", [(64, 1024, 4096, 5, 32, 8, 128),
-                                                 (7, 10, 300, 3, 28, 4, 128),
-                                                 (32, 20000, 40000, 5, 32, 8, 128),
+def run_lse(w, b):
+    out, lse = w.run(b.q, b.cache, return_lse=True)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def planted_check_with_guards(w, b, seed, progress=0):
+    """Plant keys at the device plan's segment boundaries, tile boundaries and the draft
+    block, run again on the same plan, compare with the per-request oracle (output and
+    lse), and show the check rejects zeros, a dropped causal mask and a dropped last tile
+    on these very inputs."""
+    segs = blob_of(w)["segments"]
+    AP.plant_keys(b, "causal", segments=segs, seed=seed)
+    out, lse = run_lse(w, b)
+    res = AP.oracle_per_request(b, "causal", mutations=("nomask", "droplast"), progress=progress)
+    e, m = check(out, res[None][0], lse, res[None][1])
+    say(f"  planted: max err {e:.3g} (max|ref| {m:.3g}), {len(segs)} segments, "
+        f"{int(blob_of(w)['dyn'][0])} split requests")
+    AP.assert_discriminates(res[None], [("zeros", np.zeros_like(res[None][0]), None),
+                                        ("no mask", *res["nomask"]),
+                                        ("last tile dropped", *res["droplast"])])
+
+
+def test_config2_on_device_plan():
+    """Config 2 (B=64, ctx 1k-4k, 5 causal queries, 32/8 heads, D=128) on the device
+    plan the one-graph verify step uses: plain inputs, then planted keys with guards."""
+    say("device plan, config 2: plain inputs")
+    b = config2(device=DEV)
+    w = wrapper()
+    device_plan(w, b, 5)
+    out, lse = run_lse(w, b)
+    compare_schedule(w, b, 5)
+    assert w.device_plan_error() == 0
+    ref = AP.oracle_per_request(b, "causal")[None]
+    e, m = check(out, ref[0], lse, ref[1])
+    say(f"  plain: max err {e:.3g} (max|ref| {m:.3g})")
+    say("device plan, config 2: planted keys")
+    planted_check_with_guards(w, b, seed=12)
+
+
+def test_long_contexts_on_device_plan():
+    """B=32, ctx 20k-40k on the device plan (every request split and merged through the
+    bound-sized partial slots), against the per-request fp32 oracle with planted keys
+    at the plan's segment boundaries; guards: zeros, no mask, dropped last tile."""
+    say("device plan, B=32 ctx 20k-40k: planted keys")
+    b = make_verify_batch(32, 20000, 40000, 5, 32, 8, 128, 16, dtype=torch.bfloat16, scale=0.5,
+                          seed=37, device=DEV)
+    w = wrapper()
+    device_plan(w, b, 5)
+    compare_schedule(w, b, 5)
+    assert w.device_plan_error() == 0
+    assert int(blob_of(w)["dyn"][0]) == 32, "every request should be split at this size"
+    planted_check_with_guards(w, b, seed=13, progress=8)
+
+
+@pytest.mark.parametrize("B,lo,hi,qo,hq,hkv,d", [(7, 10, 300, 3, 28, 4, 128),
                                                  (200, 1, 600, 1, 8, 2, 64)])
-def test_causal_chain_on_device_plan(B, lo, hi, qo, hq, hkv, d):
+def test_small_causal_chains_on_device_plan(B, lo, hi, qo, hq, hkv, d):
     say(f"device plan, causal chain: B={B} ctx=[{lo},{hi}] qo={qo} H={hq}/{hkv} D={d}")
     b = make_verify_batch(B, lo, hi, qo, hq, hkv, d, 16, dtype=torch.bfloat16, scale=0.5,
                           seed=B + qo).to(DEV)
     w = wrapper()
     device_plan(w, b, qo)
-    out = w.run(b.q, b.cache)
+    out, lse = run_lse(w, b)
     compare_schedule(w, b, qo)
-    if B * hi <= 2_000_000:
-        check(out, oracle(b, "causal"))
-    else:  # long contexts: the host-planned run is the reference (checked against the oracle elsewhere)
-        wh = wrapper()
-        wh.plan(b.qo_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, hq, hkv, d, 16,
-                causal=True, q_data_type=b.q.dtype)
-        ref = wh.run(b.q, b.cache).float().cpu().numpy()
-        check(out, ref)
+    ref, ref_lse = oracle(b, "causal")
+    check(out, ref, lse, ref_lse)
     assert w.device_plan_error() == 0
 
 
@@ -99,10 +149,13 @@ def test_ragged_with_empty_requests_on_device_plan():
                           ctx=ctx).to(DEV)
     w = wrapper()
     device_plan(w, b, 17)
-    out = w.run(torch.cat([b.q, torch.zeros((8 * 17 - b.q.shape[0], 32, 128), dtype=b.q.dtype,
-                                            device=DEV)]), b.cache)
+    out, lse = w.run(torch.cat([b.q, torch.zeros((8 * 17 - b.q.shape[0], 32, 128),
+                                                 dtype=b.q.dtype, device=DEV)]), b.cache,
+                     return_lse=True)
     compare_schedule(w, b, 17)
-    check(out[: b.q.shape[0]], oracle(b, "causal"))
+    n = b.q.shape[0]
+    ref, ref_lse = oracle(b, "causal")
+    check(out[:n], ref, lse[:n], ref_lse)
 
 
 def test_tree_and_streaming_on_device_plan():
@@ -112,7 +165,7 @@ def test_tree_and_streaming_on_device_plan():
     w = wrapper()
     words = torch.from_numpy(b.mask_words.view(np.int32)).to(DEV)
     device_plan(w, b, 32, causal=False, tree_mask_words=words)
-    out = w.run(b.q, b.cache)
+    out, lse = run_lse(w, b)
     compare_schedule(w, b, 32, mode=2)
     qo = np.diff(b.qo_indptr.cpu().numpy())
     flat = []
@@ -120,14 +173,16 @@ def test_tree_and_streaming_on_device_plan():
         wd = b.mask_words[b.qo_indptr[r].item(): b.qo_indptr[r + 1].item()]
         blk = ((wd[:, None].astype(np.uint64) >> np.arange(qo[r], dtype=np.uint64)) & 1).astype(bool)
         flat.append(np.concatenate([np.ones((qo[r], L - qo[r]), bool), blk], 1).ravel())
-    check(out, oracle(b, "custom", custom_mask=np.concatenate(flat)))
+    ref, ref_lse = oracle(b, "custom", custom_mask=np.concatenate(flat))
+    check(out, ref, lse, ref_lse)
 
     s = make_verify_batch(6, 2000, 9000, 1, 32, 8, 128, 16, dtype=torch.bfloat16, seed=82).to(DEV)
     w2 = wrapper()
     device_plan(w2, s, 1, sink_tokens=64, window_tokens=512)
-    out = w2.run(s.q, s.cache)
+    out, lse = run_lse(w2, s)
     compare_schedule(w2, s, 1, mode=3, sink=64, window=512)
-    check(out, oracle(s, "streaming", sink=64, window=512))
+    ref, ref_lse = oracle(s, "streaming", sink=64, window=512)
+    check(out, ref, lse, ref_lse)
 
 
 def test_graph_replays_follow_the_page_table():
@@ -190,7 +245,7 @@ def test_graph_replays_follow_the_page_table():
             if rep == 0:
                 s_cpu = s
                 s_cpu.cache = cache.cpu()
-                check(got, oracle(s_cpu, "causal"))
+                check(got, oracle(s_cpu, "causal")[0])
 
 
 def test_malformed_table_reports_and_writes_nothing():

@@ -125,29 +125,94 @@ def test_mtp_engine_construction_plan_capture_replan_replay():
     assert e.wrapper._mask_words.data_ptr() == e.custom_mask_buf.data_ptr()
 
 
-def test_replan_beyond_the_captured_shape_is_refused():
-    say("graph mode: a plan needing a larger shape after a capture raises")
-    e = Engine()
-    e.pt.insert_kv(300)
-    e.pre_draft_and_verify()
-    q = torch.zeros((MAXB * S, HQ, D), dtype=torch.bfloat16, device=DEV)
-    out = torch.empty_like(q)
+def _chain_mask(kv_lens, qo_lens):
+    """Flattened per-request bool masks: every prefix column visible, a causal block over
+    the last qo_len columns (the layout plan(custom_mask=...) accepts)."""
+    parts = []
+    for L, n in zip(kv_lens, qo_lens):
+        if n == 0:
+            continue
+        parts.append(torch.cat((torch.ones((n, L - n), dtype=torch.bool),
+                                torch.tril(torch.ones((n, n), dtype=torch.bool))), 1).flatten())
+    return torch.cat(parts).to(DEV)
+
+
+def _plan_custom(e, qo_lens):
+    """plan() with the engine's page table, causal=False and a bool custom mask for the
+    given query tokens per request (the MTP engine's call, mtp_engine.py:420-432)."""
+    qo = torch.from_numpy(np.concatenate([[0], np.cumsum(qo_lens)]).astype(np.int32)).to(DEV)
+    kvp = e.pt.paged_kv_indptr.cpu().numpy().astype(np.int64)
+    last = e.pt.paged_kv_last_page_len.cpu().numpy().astype(np.int64)
+    kv_lens = [int((kvp[b + 1] - kvp[b] - 1) * PS + last[b]) for b in range(MAXB)]
+    e.wrapper.plan(qo, e.pt.paged_kv_indptr, e.pt.paged_kv_indices, e.pt.paged_kv_last_page_len,
+                   HQ, HKV, D, PS, q_data_type=torch.bfloat16, causal=False,
+                   custom_mask=_chain_mask(kv_lens, qo_lens))
+    return qo
+
+
+def _capture(e, q, out, lse=None):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        e.wrapper.run(q, e.cache, out=out)
+        e.wrapper.run(q, e.cache, out=out, lse=lse)
     torch.cuda.current_stream().wait_stream(s)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        e.wrapper.run(q, e.cache, out=out)
+        e.wrapper.run(q, e.cache, out=out, lse=lse)
+    return graph
+
+
+def test_replan_beyond_the_captured_shape_is_refused():
+    """Same custom-mask plan arguments; only the query tokens per request grow (S + 1
+    against the captured S), so the refusal comes from the shape alone.  A plan that
+    fits the captured shape afterwards is accepted and its replay equals an eager run."""
+    say("graph mode: a plan needing a larger shape after a capture raises")
+    e = Engine()
+    e.pt.insert_kv(300)
+    e.pt.insert_kv(S + 1)
+    _plan_custom(e, [S] * MAXB)
+    q = torch.zeros((MAXB * S, HQ, D), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty_like(q)
+    graph = _capture(e, q, out)
     # the same shape with other lengths is accepted
-    e.pt.delete_kv(S)
-    e.pre_draft_and_verify()
-    # 26 query tokens per request exceed the captured 25
+    e.pt.insert_kv(7)
+    _plan_custom(e, [S] * MAXB)
+    # S + 1 query tokens per request exceed the captured S; mask and heads unchanged
     with pytest.raises(ValueError, match="captured"):
-        e.wrapper.plan(e.qo_indptr * (S + 1), e.pt.paged_kv_indptr, e.pt.paged_kv_indices,
-                       e.pt.paged_kv_last_page_len, HQ, HKV, D, PS, causal=True,
-                       q_data_type=torch.bfloat16)
+        _plan_custom(e, [S + 1] * MAXB)
+    # the refused plan left the captured shape in place: a fitting plan still replays
+    e.pt.insert_kv(3)
+    _plan_custom(e, [S] * MAXB)
+    q.copy_((torch.randn(q.shape, generator=torch.Generator().manual_seed(3)) * 0.5)
+            .to(torch.bfloat16))
+    out.zero_()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    eager = e.wrapper.run(q, e.cache)
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager)
+
+
+def test_replan_with_more_query_tokens_than_the_captured_buffers_is_refused():
+    """The captured run() read q and wrote out / lse of (MAXB - 2) * S rows (two idle
+    requests with no query tokens).  A later plan of the same fixed shape with every
+    request live has MAXB * S query tokens: replaying it would run past those buffers,
+    so plan() refuses it."""
+    say("graph mode: a plan with more query tokens than the captured q / out holds raises")
+    e = Engine()
+    e.pt.insert_kv(400)
+    e.pt.insert_kv(S)
+    live = [S] * (MAXB - 2) + [0, 0]
+    _plan_custom(e, live)
+    rows = (MAXB - 2) * S
+    q = torch.zeros((rows, HQ, D), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty_like(q)
+    lse = torch.empty((rows, HQ), dtype=torch.float32, device=DEV)
+    _capture(e, q, out, lse)
+    _plan_custom(e, live)  # the captured total is accepted again
+    with pytest.raises(ValueError, match="token rows"):
+        _plan_custom(e, [S] * MAXB)
     torch.cuda.synchronize()
 
 

@@ -154,6 +154,10 @@ def test_fixed_layout_host_plan_keeps_every_launch_argument(mode, max_qo):
         assert (s["seq"][B:, 1] == 0).all() and (s["seq"][B:, 2] == 0).all()
         assert (s["segments"][:, 0] < B).all()
         assert int(s["dyn"][2]) <= shape.num_segments
+        # merge records fit their region (one per request), partial slots their bound
+        assert int(s["dyn"][0]) <= shape.batch
+        assert shape.off_merge_seqs + 4 * int(s["dyn"][0]) <= shape.off_part_indptr
+        assert int(s["part"][-1]) <= shape.num_partials
 
 
 def test_fixed_layout_host_plan_rejects():
