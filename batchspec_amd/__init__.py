@@ -7,6 +7,8 @@ Drop-in names for the FlashInfer entry points BatchSpec calls on its verify path
   (paged KV append) and ``StandardKVCache``
 * ``sampling.chain_speculative_sampling``, ``sampling.softmax`` and the fused
   ``evaluate_posterior`` (acceptance)
+* ``ops``: the same entry points as torch custom operators (``torch.ops.bsx.*``), so a
+  ``torch.compile``-d forward keeps them in one graph
 
 All compute runs in ``libbsx.so`` (hand-written HIP for gfx950, C ABI in
 ``include/bsx.h``); the Python layer only validates, plans and launches.
@@ -16,7 +18,7 @@ from .page import (StandardKVCache, append_kv, append_paged_kv_cache,
                    get_batch_indices_positions, get_seq_lens)
 from .page_table import DevicePageTable
 from .posterior import PosteriorMixin, evaluate_posterior
-from . import masks, sampling
+from . import masks, ops, sampling
 
 __all__ = [
     "BatchPrefillWithPagedKVCacheWrapper",
@@ -29,5 +31,6 @@ __all__ = [
     "PosteriorMixin",
     "evaluate_posterior",
     "masks",
+    "ops",
     "sampling",
 ]

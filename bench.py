@@ -25,10 +25,11 @@ Printed: one JSON line with
               `spaced`: the same runs separated by short idle gaps, which keep the
               shader clock unthrottled; back-to-back it settles lower under the power
               limit)
-  accepted_tok_s  accepted tokens/s of a 32-layer verify step: the page-table update
-              (insert + delete), one device plan, 32 x (append + attention) and the
-              fused greedy acceptance over [64, 5, 128256] bf16 logits (draft = target
-              argmax with probability 0.7), reference acceptance rule;
+  accepted_tok_s  accepted tokens/s of a 32-layer verify step captured in one graph
+              and replayed (verify_step_graph): the page-table insert, one device plan,
+              32 x (append + attention, a KV cache per layer), the fused greedy
+              acceptance over [64, 5, 128256] bf16 logits (draft = target argmax with
+              probability 0.7, reference rule) and the delete of rejected tokens;
               accepted_tok_s_sampling the same step with the reference's default
               sampling acceptance instead (sampling_accept_mtp: T=0.6, top_k=20,
               top_p=0.95, one-hot drafts, accept = emitted + 1)
@@ -59,6 +60,10 @@ PROFILES = ROOT / "profiles"
 TRAFFIC_FILE = PROFILES / "verify_attn_config2_traffic.txt"
 MFMA_FILE = PROFILES / "verify_attn_mfma_counters.txt"
 NUM_LAYERS = 32
+# distinct input buffers the timed loops rotate through, so that the 256 MB memory-side
+# cache (MALL) cannot serve a call's reads from the previous calls
+ROTATE_ACCEPT = 5   # 5 x 82 MB of [64, 5, 128256] bf16 logits
+ROTATE_3A = 5       # 5 x 76 MB of sink + window views
 
 
 def attn_bytes(b) -> int:
@@ -205,8 +210,9 @@ def config3a_attention(dev, iters):
     import numpy as np
     import torch
     from batchspec_amd.workloads import make_verify_batch
+    # five sets (5 x 76 MB of views, more than the 256 MB memory-side cache) in turn
     s3a = [make_verify_batch(32, 32768, 65536, 1, 32, 8, 128, 16, dtype=torch.bfloat16,
-                             scale=0.5, seed=1003 + i, device=dev) for i in range(2)]
+                             scale=0.5, seed=1003 + i, device=dev) for i in range(ROTATE_3A)]
 
     def view_bytes(b):  # K/V rows of the 64 + 512 view, Q, O, page ids of the view
         view = int(np.sum(np.minimum(b.kv_lens, 576)))
@@ -215,6 +221,7 @@ def config3a_attention(dev, iters):
     wr, us = attention_pass(dev, s3a, dict(causal=True, sink_tokens=64, window_tokens=512), iters)
     rec = pass_record(wr, us, mean([view_bytes(b) for b in s3a]))
     rec["workload"] = "B=32, ctx U[32768,65536], 1 query over a 64-sink + 512-window view"
+    rec["rotating_sets"] = ROTATE_3A
     return rec
 
 
@@ -225,8 +232,12 @@ def acceptance(dev, iters, out):
     from batchspec_amd.workloads import greedy_case, stochastic_case
     g = greedy_case(B=64, k=4, V=128256, p_match=0.7, seed=2002, dtype=torch.bfloat16)
     gl, gd = g.target_logits.to(dev), g.draft_tokens.to(dev)
-    acc_us = time_events(lambda i: bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1),
-                         iters, 3)
+    # ROTATE distinct copies of the logits (5 x 82 MB = 410 MB, more than the 256 MB
+    # memory-side cache), so no timed call finds its rows left in that cache by the
+    # previous one
+    gls = [gl] + [gl.clone() for _ in range(ROTATE_ACCEPT - 1)]
+    acc_us = time_events(lambda i: bsx.evaluate_posterior(gd, gls[i % ROTATE_ACCEPT], greedy=True,
+                                                          eos_token_id=-1), iters, 3)
     _, acc_ref, _ = bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1)
     _, acc_pre, _ = bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1,
                                            accept_rule="prefix")
@@ -241,11 +252,11 @@ def acceptance(dev, iters, out):
     # the same logits and drafts
     gu = g.uniforms.to(dev)
 
-    def sampling_accept():
+    def sampling_accept(i=0):
         return bsx.sampling.chain_speculative_sampling_from_logits(
-            None, gd, gl, 0.6, uniforms=gu, top_k=20, top_p=0.95)
+            None, gd, gls[i % ROTATE_ACCEPT], 0.6, uniforms=gu, top_k=20, top_p=0.95)
 
-    samp_us = time_events(lambda i: sampling_accept(), iters, 3)
+    samp_us = time_events(sampling_accept, iters, 3)
     acc_samp = sampling_accept()[2] + 1
     t_samp = mean(samp_us)
     out["sampling_accept_mtp"] = {
@@ -253,21 +264,27 @@ def acceptance(dev, iters, out):
         "frac": round(gbytes / t_samp / 1e3 / HBM_PEAK_GBS, 4), "bytes": gbytes,
         "workload": "[64, 5, 128256] bf16 target logits, one-hot drafts, T=0.6, top_k=20, "
                     "top_p=0.95"}
-    del gl, g
+    out["greedy_accept"]["rotating_buffers"] = ROTATE_ACCEPT
+    out["sampling_accept_mtp"]["rotating_buffers"] = ROTATE_ACCEPT
+    del gl, gls, g
     s = stochastic_case(device=dev)
+    # two distinct copies of config 5's 361 MB of logits, used in turn
+    tls = [s.target_logits, s.target_logits.clone()]
+    dls = [s.draft_logits, s.draft_logits.clone()]
     n = max(5, iters // 3)
     st_us = time_events(lambda i: bsx.sampling.chain_speculative_sampling_from_logits(
-        s.draft_logits, s.draft_tokens, s.target_logits, 1.0, uniforms=s.uniforms), n, 2)
+        dls[i % 2], s.draft_tokens, tls[i % 2], 1.0, uniforms=s.uniforms), n, 2)
     t_st = mean(st_us)
     sbytes = (s.target_logits.numel() + s.draft_logits.numel()) * 2
     out["stochastic_accept"] = {"us": round(t_st, 2), "GB/s": round(sbytes / t_st / 1e3, 1),
                                 "frac": round(sbytes / t_st / 1e3 / HBM_PEAK_GBS, 4),
                                 "bytes": sbytes,
-                                "workload": "config 5: B=128, k=5, V=128256 bf16, T=1, draft logits"}
+                                "workload": "config 5: B=128, k=5, V=128256 bf16, T=1, draft logits",
+                                "rotating_buffers": 2}
     # the same acceptance with the reference's default filters (top_k=20, top_p=0.95)
     # applied to both distributions
     sf_us = time_events(lambda i: bsx.sampling.chain_speculative_sampling_from_logits(
-        s.draft_logits, s.draft_tokens, s.target_logits, 1.0, uniforms=s.uniforms,
+        dls[i % 2], s.draft_tokens, tls[i % 2], 1.0, uniforms=s.uniforms,
         top_k=20, top_p=0.95), n, 2)
     t_sf = mean(sf_us)
     out["stochastic_accept_top_k20_top_p095"] = {
@@ -277,7 +294,7 @@ def acceptance(dev, iters, out):
     # many to list, so the threshold comes from the exponent-bin select (three reads of
     # each row; "frac" counts one)
     sp_us = time_events(lambda i: bsx.sampling.chain_speculative_sampling_from_logits(
-        s.draft_logits, s.draft_tokens, s.target_logits, 1.0, uniforms=s.uniforms,
+        dls[i % 2], s.draft_tokens, tls[i % 2], 1.0, uniforms=s.uniforms,
         top_p=0.95), n, 2)
     t_sp = mean(sp_us)
     out["stochastic_accept_top_p095"] = {
@@ -358,6 +375,102 @@ def step_plumbing(dev, iters, sets, acc_ref):
     out["collate_accepted_kv"] = {"us_3_layers": round(t_col, 2), "bytes_moved": moved,
                                   "GB/s": round(moved / t_col / 1e3, 1)}
     return out
+
+
+def verify_step_graph(dev, iters):
+    """One verify step as BatchSpec runs it (mtp_engine.py:716-774 with the chain draft
+    of config 2), captured in one graph and replayed: DevicePageTable.insert_kv of the 5
+    draft tokens, one device plan, 32 layers of (paged append + verify attention), each
+    layer with its own KV cache, then the acceptance over [64, 5, 128256] bf16 logits
+    and delete_kv of the rejected tokens.  Two graphs: greedy acceptance (draft = target
+    argmax with probability 0.7, reference rule) and the reference's default sampling
+    acceptance (T=0.6, top_k=20, top_p=0.95, one-hot drafts).  Returns per graph the
+    replay's GPU time and the tokens it accepted."""
+    import numpy as np
+    import torch
+    import batchspec_amd as bsx
+    from batchspec_amd.page_table import DevicePageTable
+    from batchspec_amd.workloads import greedy_case
+    B, K, HQ, HKV, D, PS = 64, 4, 32, 8, 128, 16
+    S = K + 1
+    g = greedy_case(B=B, k=K, V=128256, p_match=0.7, seed=2002, dtype=torch.bfloat16)
+    gl, gd, gu = g.target_logits.to(dev), g.draft_tokens.to(dev), g.uniforms.to(dev)
+    rng = np.random.default_rng(1002)
+    ctx = rng.integers(1024, 4097, B).astype(np.int32)
+    replays = 2 * (iters + 8)
+    max_pages = (4096 + S * replays + PS - 1) // PS + 2
+    pt = DevicePageTable(PS, B, max_pages, dev)
+    pt.insert_kv(torch.from_numpy(ctx).to(dev))
+    gen = torch.Generator(device=dev).manual_seed(1002)
+
+    def randn(*shape):
+        x = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+        for c in x.view(shape[0], -1).split(4096):
+            c.copy_(torch.randn(c.shape, generator=gen, device=dev) * 0.5)
+        return x
+    caches = [randn(B * max_pages, 2, PS, HKV, D) for _ in range(NUM_LAYERS)]
+    qs = [randn(B * S, HQ, D) for _ in range(NUM_LAYERS)]
+    ks = [randn(B * S, HKV, D) for _ in range(NUM_LAYERS)]
+    vs = [randn(B * S, HKV, D) for _ in range(NUM_LAYERS)]
+    outs = [torch.empty_like(q) for q in qs]
+    qo_indptr = torch.arange(B + 1, dtype=torch.int32, device=dev) * S
+    w = bsx.BatchPrefillWithPagedKVCacheWrapper(
+        torch.empty(256 << 20, dtype=torch.uint8, device=dev), "NHD", use_cuda_graph=True,
+        qo_indptr_buf=qo_indptr, paged_kv_indptr_buf=pt.paged_kv_indptr,
+        paged_kv_indices_buf=pt.paged_kv_indices,
+        paged_kv_last_page_len_buf=pt.paged_kv_last_page_len)
+    accept_buf = torch.zeros(B, dtype=torch.int64, device=dev)
+
+    def step(mode):
+        pt.insert_kv(S)
+        w.plan(qo_indptr, pt.paged_kv_indptr, pt.paged_kv_indices, pt.paged_kv_last_page_len,
+               HQ, HKV, D, PS, causal=True, q_data_type=torch.bfloat16, on_device=True,
+               max_qo_len=S)
+        for layer in range(NUM_LAYERS):
+            bsx.append_kv(ks[layer], vs[layer], qo_indptr, caches[layer], pt.paged_kv_indptr,
+                          pt.paged_kv_indices, pt.paged_kv_last_page_len)
+            w.run(qs[layer], caches[layer], out=outs[layer])
+        if mode == "greedy":
+            _, acc, _ = bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1)
+        else:
+            acc = bsx.sampling.chain_speculative_sampling_from_logits(
+                None, gd, gl, 0.6, uniforms=gu, top_k=20, top_p=0.95)[2] + 1
+        accept_buf.copy_(acc)
+        pt.delete_kv(S - acc)
+
+    res = {}
+    for mode in ("greedy", "sampling"):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step(mode)  # warm-up outside the graph
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(mode)
+        torch.cuda.synchronize()
+        us = time_events(lambda i: graph.replay(), iters, 3)
+        accepted = int(accept_buf.sum())
+        pt.check()
+        err = w.device_plan_error()
+        if err != 0:
+            raise RuntimeError(f"verify step graph: device plan error {err}")
+        res[mode] = {"us": round(mean(us), 1), "us_median": round(median(us), 1),
+                     "accepted_tokens": accepted,
+                     "accepted_tok_s": round(accepted / (mean(us) * 1e-6), 1)}
+        del graph
+    cl = pt.cachelens.cpu().numpy()
+    res["workload"] = ("one captured graph per acceptance mode: insert_kv(5), device plan, "
+                       f"{NUM_LAYERS} x (append + verify attention, a KV cache per layer), "
+                       "acceptance over [64, 5, 128256] bf16 logits, delete_kv; B=64, ctx "
+                       "U[1024,4096] at the start, growing by the accepted tokens each replay; "
+                       "page ids from the DevicePageTable allocator (request r holds pages "
+                       "r*max_pages + k)")
+    res["cachelens_after"] = [int(cl.min()), int(cl.max())]
+    del caches
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_threads() -> int:
@@ -621,21 +734,26 @@ def main() -> int:
             result.update(plumbing)
             t_plan = plumbing["config2_device_plan"]["plan_kernel_us"]
             t_pt = plumbing["page_table_step"]["us"]
-            t_host = plumbing["config2_device_plan"]["host_plan_wall_us_median"]
-            t_model = t_pt + t_plan + NUM_LAYERS * (t_attn + t_app) + t_acc
+            t_attn_dev = plumbing["config2_device_plan"]["attention_us"]
+            log("the verify step captured in one graph: 32 layers, greedy and sampling")
+            vs = verify_step_graph(dev, args.steps)
+            result["verify_step_graph"] = vs
             n_ref, n_pre = int(acc_ref.sum()), int(acc_pre.sum())
-            result["accepted_tok_s"] = round(n_ref / (t_model * 1e-6), 1)
-            result["accepted_tok_s_prefix_rule"] = round(n_pre / (t_model * 1e-6), 1)
-            result["accepted_tok_s_host_plan"] = round(
-                n_ref / ((t_model - t_plan + t_host) * 1e-6), 1)
-            t_model_s = t_model - t_acc + t_samp
             n_samp = int(acc_samp.sum())
-            result["accepted_tok_s_sampling"] = round(n_samp / (t_model_s * 1e-6), 1)
+            # accepted tokens per second of the replayed step (the logits and drafts are
+            # the acceptance's own, so each replay accepts the same tokens)
+            result["accepted_tok_s"] = vs["greedy"]["accepted_tok_s"]
+            result["accepted_tok_s_sampling"] = vs["sampling"]["accepted_tok_s"]
+            result["accepted_tok_s_prefix_rule"] = round(
+                n_pre / (vs["greedy"]["us"] * 1e-6), 1)
             result["mean_accept_len"] = {"reference_rule": n_ref / 64, "prefix_rule": n_pre / 64,
                                          "sampling": n_samp / 64}
-            result["verify_step_us"] = {
-                "total": round(t_model, 1), "page_table": t_pt, "device_plan": t_plan,
-                "layers_attention_append": round(NUM_LAYERS * (t_attn + t_app), 1),
+            # the same step as a sum of the separately timed parts, attention on the device
+            # plan (a breakdown of the replay above, not the source of accepted_tok_s)
+            t_parts = t_pt + t_plan + NUM_LAYERS * (t_attn_dev + t_app) + t_acc
+            result["verify_step_parts_us"] = {
+                "sum_greedy": round(t_parts, 1), "page_table": t_pt, "device_plan": t_plan,
+                "layers_attention_append": round(NUM_LAYERS * (t_attn_dev + t_app), 1),
                 "greedy_accept": round(t_acc, 2), "sampling_accept": round(t_samp, 2),
                 "layers": NUM_LAYERS}
 
