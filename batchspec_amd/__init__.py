@@ -17,7 +17,7 @@ from .attention import BatchPrefillWithPagedKVCacheWrapper
 from .page import (StandardKVCache, append_kv, append_paged_kv_cache,
                    get_batch_indices_positions, get_seq_lens)
 from .page_table import DevicePageTable
-from .posterior import PosteriorMixin, evaluate_posterior
+from .posterior import PosteriorMixin, evaluate_posterior, evaluate_posterior_and_delete
 from . import masks, ops, sampling
 
 __all__ = [
@@ -30,6 +30,7 @@ __all__ = [
     "DevicePageTable",
     "PosteriorMixin",
     "evaluate_posterior",
+    "evaluate_posterior_and_delete",
     "masks",
     "ops",
     "sampling",

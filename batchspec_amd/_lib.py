@@ -112,6 +112,9 @@ SIGNATURES = {
     "bsx_tree_masks": (c_int, [_P, c_int64, c_int, _P, c_int, _P, _P, _P]),
     "bsx_page_table_update": (c_int, [_P, _P, _P, _P, c_int32, c_int, c_int, c_int, c_int, _P, _P,
                                       _P, _P]),
+    "bsx_accept_greedy_delete": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int64, c_int64, c_int,
+                                         _P, _P, _P, _P, c_int64, c_int32, _P, _P, _P, c_int, c_int,
+                                         _P, _P, _P]),
     "bsx_filter_ws_bytes": (c_int64, [c_int64]),
     "bsx_chain_filtered_ws_bytes": (c_int64, [c_int, c_int, c_int64]),
     "bsx_chain_speculative_sampling_filtered": (c_int, [_P, _P, _P, c_int, c_float, c_int, c_float,
@@ -123,6 +126,7 @@ SIGNATURES = {
     "bsx_sample_ws_bytes": (c_int64, [c_int64, c_int64]),
     "bsx_sample": (c_int, [_P, c_int, c_float, c_int, c_float, _P, c_int64, c_int64, _P, _P,
                            c_int64, _P]),
+    "bsx_read_probe": (c_int, [_P, c_int64, c_int, c_int, _P, _P]),
     "bsx_softmax_ws_bytes": (c_int64, [c_int64]),
     "bsx_softmax": (c_int, [_P, c_int, c_float, c_int64, c_int64, _P, _P, c_int64, _P]),
 }

@@ -41,6 +41,7 @@ HIP_SOURCES = {
     "masks.hip": [],
     "page_table.hip": [],
     "plan_device.hip": [],
+    "probe.hip": [],
     "accept.hip": ["-ffp-contract=off"],
     "filter.hip": ["-ffp-contract=off"],
 }

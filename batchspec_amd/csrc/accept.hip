@@ -26,6 +26,7 @@
 
 #include "common.h"
 #include "canon.h"
+#include "page_update.h"
 #include "rows.h"
 
 namespace bsx {
@@ -740,6 +741,66 @@ __global__ void __launch_bounds__(256) greedy_eval_kernel(
   }
 }
 
+// Greedy acceptance evaluated inside the page-table delete that consumes its accept
+// counts (the verify step's next operation: delete_kv(n_inserted - accept_nums)), one
+// workgroup of pt::kThreads threads.  The waves evaluate the requests, packed: lane l of
+// a wave holds request slot l / (k+1) and row l % (k+1), so a wave covers 64 / (k+1)
+// requests per round (12 at k = 4) and every request of the step is evaluated in one
+// round of partial loads; the accept counts stay in LDS for the delete, which is
+// page_table_kernel's update (page_update.h) with d_r = n_inserted - accept_r.
+constexpr int kFusedMaxBatch = 8192;
+
+__global__ void __launch_bounds__(pt::kThreads) greedy_eval_delete_kernel(
+    const int64_t* draft, const int64_t* target_ids, const float* pval, const int32_t* pcol,
+    int64_t parts, int B, int k, int64_t eos, int mode, int64_t* bonus, int64_t* accept,
+    uint8_t* eos_acc, int32_t n_inserted, pt::Args pa) {
+  __shared__ int32_t s_acc[kFusedMaxBatch];
+  constexpr int NW = pt::kThreads / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int R = k + 1;
+  const int per_wave = 64 / R;
+  const int slot = lane / R;
+  const int i = lane - slot * R;
+  const int sbit = slot * R;  // <= 63
+  const uint64_t seg_mask = R >= 64 ? ~0ull : ((1ull << R) - 1);
+  for (int b0 = wave * per_wave; b0 < B; b0 += NW * per_wave) {
+    const int b = b0 + slot;
+    const bool active = slot < per_wave && b < B;
+    int64_t pred = -1;
+    if (active) {
+      const int64_t r = (int64_t)b * R + i;
+      pred = target_ids ? target_ids[r] : row_argmax(pval, pcol, r, parts);
+    }
+    const int64_t d = active && i < k ? draft[(int64_t)b * k + i] : -2;
+    const bool flag = active && i < k && pred == d;
+    const uint64_t seg = (__builtin_amdgcn_ballot_w64(flag) >> sbit) & seg_mask;
+    int n;
+    uint64_t counted;
+    if (mode == 0) {
+      counted = seg;
+      n = __builtin_popcountll(seg);
+    } else {
+      // longest matching prefix: the run of ones from the request's row 0
+      const uint64_t miss = ~seg;
+      n = miss ? __builtin_ctzll(miss) : 64;
+      counted = n >= 64 ? ~0ull : ((1ull << n) - 1);
+    }
+    const bool my_counted = i < 64 && ((counted >> i) & 1ull);
+    const uint64_t eh =
+        (__builtin_amdgcn_ballot_w64(active && my_counted && d == eos) >> sbit) & seg_mask;
+    const int64_t bonus_v = __shfl(pred, min(sbit + n, 63));
+    if (active && i == 0) {
+      accept[b] = n + 1;
+      bonus[b] = bonus_v;
+      eos_acc[b] = eh ? 1 : 0;
+      s_acc[b] = n + 1;
+    }
+  }
+  __syncthreads();
+  pt::update_pages(pa, [&](int r) -> int32_t { return n_inserted - s_acc[r]; });
+}
+
 static int elem_bytes_of(int dtype) { return dtype == BSX_DTYPE_FP32 ? 4 : 2; }
 
 static int dispatch_argmax_parts(const void* logits, int dtype, int64_t rows, int64_t V,
@@ -853,6 +914,65 @@ extern "C" int bsx_accept_greedy(const int64_t* draft_d, const int64_t* target_i
   hipLaunchKernelGGL(acc::greedy_eval_kernel, dim3((unsigned)ceil_div(B, 4)), dim3(256), 0, st,
                      draft_d, target_ids_d, pv, pc, sp.parts, B, k, eos_id, mode, bonus_d,
                      accept_d, eos_acc_d);
+  BSX_LAUNCH_CHECK();
+  return BSX_OK;
+}
+
+extern "C" int bsx_accept_greedy_delete(
+    const int64_t* draft_d, const int64_t* target_ids_d, const void* target_logits_d, int dtype,
+    int B, int k, int64_t vocab, int64_t eos_id, int mode, int64_t* bonus_d, int64_t* accept_d,
+    uint8_t* eos_acc_d, void* ws_d, int64_t ws_bytes, int32_t n_inserted, int32_t* num_pages_d,
+    int32_t* last_len_d, int32_t* cachelens_d, int page_size, int max_pages, int32_t* indptr_d,
+    int32_t* indices_d, void* stream) {
+  BSX_REQUIRE(B >= 0 && k >= 0 && k <= 63, BSX_ERR_INVALID, "bad B=%d / k=%d (k <= 63)", B, k);
+  BSX_REQUIRE(mode == 0 || mode == 1, BSX_ERR_INVALID, "mode must be 0 or 1");
+  if (B == 0) return BSX_OK;
+  BSX_REQUIRE(B <= acc::kFusedMaxBatch, BSX_ERR_UNSUPPORTED,
+              "the fused acceptance + delete takes at most %d requests (got %d)",
+              acc::kFusedMaxBatch, B);
+  BSX_REQUIRE(n_inserted >= k + 1, BSX_ERR_INVALID,
+              "n_inserted (%d) must cover the k + 1 = %d verified tokens", n_inserted, k + 1);
+  BSX_REQUIRE(bonus_d && accept_d && eos_acc_d && (k == 0 || draft_d), BSX_ERR_INVALID,
+              "null pointer");
+  BSX_REQUIRE(target_ids_d || target_logits_d, BSX_ERR_INVALID, "need target ids or logits");
+  BSX_REQUIRE(page_size > 0 && max_pages > 0, BSX_ERR_INVALID, "bad page_size or max_pages");
+  BSX_REQUIRE((int64_t)B * max_pages < (1LL << 31), BSX_ERR_UNSUPPORTED, "page table too large");
+  BSX_REQUIRE(num_pages_d && last_len_d && indptr_d && indices_d, BSX_ERR_INVALID,
+              "null page-table pointer");
+  hipStream_t st = as_stream(stream);
+  const int64_t rows = (int64_t)B * (k + 1);
+  float* pv = nullptr;
+  int32_t* pc = nullptr;
+  acc::ArgmaxSplit sp = {1, 8};
+  if (!target_ids_d) {
+    BSX_REQUIRE(vocab > 0 && vocab < (1LL << 31), BSX_ERR_INVALID, "vocab must be in (0, 2^31)");
+    BSX_REQUIRE(ws_d && ws_bytes >= bsx_accept_greedy_ws_bytes(B, k, vocab), BSX_ERR_CAPACITY,
+                "greedy workspace too small");
+    BSX_REQUIRE(dtype == BSX_DTYPE_BF16 || dtype == BSX_DTYPE_FP16 || dtype == BSX_DTYPE_FP32,
+                BSX_ERR_INVALID, "unknown dtype %d", dtype);
+    sp = acc::argmax_split(rows, vocab, acc::elem_bytes_of(dtype));
+    BSX_REQUIRE(rows * sp.parts < (1LL << 31), BSX_ERR_UNSUPPORTED, "too many rows for one launch");
+    pv = reinterpret_cast<float*>(static_cast<char*>(ws_d) + argmax_values_offset());
+    pc = reinterpret_cast<int32_t*>(static_cast<char*>(ws_d) + argmax_columns_offset(rows, vocab));
+    int rc = acc::dispatch_argmax_parts(target_logits_d, dtype, rows, vocab, vocab, sp, pv, pc, st);
+    if (rc != BSX_OK) return rc;
+  }
+  pt::Args pa;
+  pa.num_pages = num_pages_d;
+  pa.last_len = last_len_d;
+  pa.cachelens = cachelens_d;
+  pa.d = nullptr;
+  pa.d_scalar = 0;
+  pa.sign = -1;
+  pa.B = B;
+  pa.page_size = page_size;
+  pa.max_pages = max_pages;
+  pa.indptr = indptr_d;
+  pa.indices = indices_d;
+  pa.errors = nullptr;  // a delete never exceeds the page budget
+  hipLaunchKernelGGL(acc::greedy_eval_delete_kernel, dim3(1), dim3(pt::kThreads), 0, st, draft_d,
+                     target_ids_d, pv, pc, sp.parts, B, k, eos_id, mode, bonus_d, accept_d,
+                     eos_acc_d, n_inserted, pa);
   BSX_LAUNCH_CHECK();
   return BSX_OK;
 }

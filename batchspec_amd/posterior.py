@@ -80,6 +80,51 @@ def _greedy(draft: torch.Tensor, preds: torch.Tensor, eos: int, mode: int):
     return bonus[:, None], accept, eos_acc.view(torch.bool)[:, None]
 
 
+def evaluate_posterior_and_delete(draft_tokens: torch.Tensor, target_preds: torch.Tensor,
+                                  page_table, n_inserted: int, *, eos_token_id: int,
+                                  accept_rule: str = "reference"
+                                  ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Greedy ``evaluate_posterior`` (mtp_engine.py:553-560) followed by
+    ``page_table.delete_kv(n_inserted - accept_nums)`` (page_table.py:95-137), the
+    verify step's next operation, in one argmax launch (for logits) and one kernel that
+    evaluates every request and updates the DevicePageTable.  Same outputs and table
+    state as the two calls in sequence; n_inserted >= k + 1 is the number of tokens the
+    step inserted per request."""
+    dev = require_gpu("evaluate_posterior_and_delete", draft_tokens, target_preds)
+    B, k = draft_tokens.shape
+    if page_table.max_batch_size != B:
+        raise ValueError(f"page table holds {page_table.max_batch_size} requests, drafts {B}")
+    d = draft_tokens.to(torch.int64).contiguous()
+    bonus = torch.empty(B, dtype=torch.int64, device=dev)
+    accept = torch.empty(B, dtype=torch.int64, device=dev)
+    eos_acc = torch.empty(B, dtype=torch.uint8, device=dev)
+    lib = _lib.load()
+    ids = logits = None
+    V, dt, ws = 0, 0, None
+    if target_preds.dim() == 2:
+        if target_preds.shape != (B, k + 1):
+            raise ValueError(f"target ids must be [B, k+1], got {tuple(target_preds.shape)}")
+        ids = target_preds.to(torch.int64).contiguous()
+    elif target_preds.dim() == 3:
+        if target_preds.shape[:2] != (B, k + 1):
+            raise ValueError(f"target logits must be [B, k+1, V], got {tuple(target_preds.shape)}")
+        logits = target_preds.contiguous()
+        V, dt = logits.shape[2], dtype_code(logits.dtype)
+        ws = workspace(dev, int(lib.bsx_accept_greedy_ws_bytes(B, k, V)), _WS, f"greedy:{dev}")
+    else:
+        raise ValueError("target_preds must be ids [B, k+1] or logits [B, k+1, V]")
+    pt = page_table
+    rc = lib.bsx_accept_greedy_delete(
+        d.data_ptr(), _lib.ptr(ids), _lib.ptr(logits), dt, B, k, V, int(eos_token_id),
+        _RULES[accept_rule], bonus.data_ptr(), accept.data_ptr(), eos_acc.data_ptr(),
+        _lib.ptr(ws), 0 if ws is None else ws.numel(), int(n_inserted),
+        pt.page_manager.num_allocated_pages.data_ptr(), pt.paged_kv_last_page_len.data_ptr(),
+        pt.cachelens.data_ptr(), pt.page_size, pt.max_num_pages_per_request,
+        pt.paged_kv_indptr.data_ptr(), pt.paged_kv_indices.data_ptr(), stream_of(dev))
+    _lib.check(rc, "evaluate_posterior_and_delete")
+    return bonus[:, None], accept, eos_acc.view(torch.bool)[:, None]
+
+
 class PosteriorMixin:
     """Engine mixin with the reference's method signature; reads ``greedy``,
     ``eos_token_id``, ``temperature``, ``top_p``, ``top_k`` from the engine."""

@@ -39,7 +39,9 @@ Printed: one JSON line with
 
 `--only NAME` (attn2, accept, attn4, attn3b, attn3a) times one part alone, for the
 counter runs of rocprofv3; `--calibrate-copy` times a plain 1 GiB device copy (the
-known-size kernel the HBM byte counters are scaled against).
+known-size kernel the HBM byte counters are scaled against); `--calibrate-read` times a
+one-pass read of the greedy logits (bsx_read_probe) in several launch shapes beside the
+greedy acceptance on the same rotating buffers.
 """
 from __future__ import annotations
 
@@ -246,6 +248,36 @@ def acceptance(dev, iters, out):
     out["greedy_accept"] = {"us": round(t_acc, 2), "GB/s": round(gbytes / t_acc / 1e3, 1),
                             "frac": round(gbytes / t_acc / 1e3 / HBM_PEAK_GBS, 4),
                             "bytes": gbytes, "workload": "[64, 5, 128256] bf16 logits, fused argmax"}
+    # the acceptance with the delete of rejected tokens it feeds (a verify step inserts 5
+    # tokens per request first, so each timed call starts with that insert): two calls
+    # (evaluate_posterior, delete_kv) against the fused entry point
+    import numpy as np
+    from batchspec_amd.page_table import DevicePageTable
+    pt = DevicePageTable(16, 64, 300, dev)
+    pt.insert_kv(torch.from_numpy(np.random.default_rng(7).integers(1024, 4096, 64)
+                                  .astype(np.int32)).to(dev))
+
+    def insert_only(i):
+        pt.insert_kv(5)
+
+    def two_calls(i):
+        pt.insert_kv(5)
+        _, a, _ = bsx.evaluate_posterior(gd, gls[i % ROTATE_ACCEPT], greedy=True, eos_token_id=-1)
+        pt.delete_kv(5 - a)
+
+    def fused(i):
+        pt.insert_kv(5)
+        bsx.evaluate_posterior_and_delete(gd, gls[i % ROTATE_ACCEPT], pt, 5, eos_token_id=-1)
+    t_two = mean(time_events(two_calls, iters, 3))
+    t_fused = mean(time_events(fused, iters, 3))
+    t_ins = mean(time_events(insert_only, iters, 3))
+    pt.check()
+    out["greedy_accept_delete"] = {
+        "insert_accept_delete_us": {"two_calls": round(t_two, 2), "fused": round(t_fused, 2)},
+        "insert_us": round(t_ins, 2),
+        "workload": "DevicePageTable B=64: insert_kv(5), then greedy acceptance over [64, 5, "
+                    "128256] bf16 logits and delete_kv(5 - accept), as evaluate_posterior + "
+                    "delete_kv or as evaluate_posterior_and_delete"}
     # the reference's default sampling mode (temperature 0.6, top_k 20, top_p 0.95;
     # batchspec/args.py:104-116) as the MTP branch of evaluate_posterior runs it
     # (mtp_engine.py:561-575: filtered target, one-hot drafts, accept = emitted + 1), on
@@ -382,10 +414,12 @@ def verify_step_graph(dev, iters):
     of config 2), captured in one graph and replayed: DevicePageTable.insert_kv of the 5
     draft tokens, one device plan, 32 layers of (paged append + verify attention), each
     layer with its own KV cache, then the acceptance over [64, 5, 128256] bf16 logits
-    and delete_kv of the rejected tokens.  Two graphs: greedy acceptance (draft = target
-    argmax with probability 0.7, reference rule) and the reference's default sampling
-    acceptance (T=0.6, top_k=20, top_p=0.95, one-hot drafts).  Returns per graph the
-    replay's GPU time and the tokens it accepted."""
+    and delete_kv of the rejected tokens.  Three graphs: greedy acceptance (draft = target
+    argmax with probability 0.7, reference rule) fused with the delete
+    (evaluate_posterior_and_delete), the same as two calls (evaluate_posterior, then
+    delete_kv), and the reference's default sampling acceptance (T=0.6, top_k=20,
+    top_p=0.95, one-hot drafts).  Returns per graph the replay's GPU time and the tokens
+    it accepted."""
     import numpy as np
     import torch
     import batchspec_amd as bsx
@@ -397,7 +431,7 @@ def verify_step_graph(dev, iters):
     gl, gd, gu = g.target_logits.to(dev), g.draft_tokens.to(dev), g.uniforms.to(dev)
     rng = np.random.default_rng(1002)
     ctx = rng.integers(1024, 4097, B).astype(np.int32)
-    replays = 2 * (iters + 8)
+    replays = iters + 8
     max_pages = (4096 + S * replays + PS - 1) // PS + 2
     pt = DevicePageTable(PS, B, max_pages, dev)
     pt.insert_kv(torch.from_numpy(ctx).to(dev))
@@ -431,6 +465,11 @@ def verify_step_graph(dev, iters):
                           pt.paged_kv_indices, pt.paged_kv_last_page_len)
             w.run(qs[layer], caches[layer], out=outs[layer])
         if mode == "greedy":
+            # the acceptance and the delete it feeds in one argmax + one kernel
+            _, acc, _ = bsx.evaluate_posterior_and_delete(gd, gl, pt, S, eos_token_id=-1)
+            accept_buf.copy_(acc)
+            return
+        if mode == "greedy_unfused":
             _, acc, _ = bsx.evaluate_posterior(gd, gl, greedy=True, eos_token_id=-1)
         else:
             acc = bsx.sampling.chain_speculative_sampling_from_logits(
@@ -438,8 +477,15 @@ def verify_step_graph(dev, iters):
         accept_buf.copy_(acc)
         pt.delete_kv(S - acc)
 
+    # every mode starts from the same page-table state (each replay grows the contexts by
+    # the accepted tokens), so the graphs are timed over the same lengths
+    state = [pt.cachelens, pt.page_manager.num_allocated_pages, pt.paged_kv_last_page_len,
+             pt.paged_kv_indptr, pt.paged_kv_indices]
+    snapshot = [x.clone() for x in state]
     res = {}
-    for mode in ("greedy", "sampling"):
+    for mode in ("greedy", "greedy_unfused", "sampling"):
+        for x, y in zip(state, snapshot):
+            x.copy_(y)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -589,6 +635,48 @@ def calibrate_copy(reps: int = 5) -> int:
     return 0
 
 
+def calibrate_read(iters: int = 20) -> int:
+    """The floor of a one-pass read of the greedy acceptance's logits: bsx_read_probe over
+    [64, 5, 128256] bf16 (82 MB) in several launch shapes, rotating 5 distinct buffers
+    (410 MB, more than the memory-side cache), beside the greedy acceptance (argmax +
+    evaluation) and its argmax kernel alone on the same buffers."""
+    import torch
+    import batchspec_amd as bsx
+    from batchspec_amd import _lib
+    from batchspec_amd.workloads import greedy_case
+    dev = "cuda:0"
+    lib = _lib.load()
+    g = greedy_case(B=64, k=4, V=128256, p_match=0.7, seed=2002, dtype=torch.bfloat16)
+    gl, gd = g.target_logits.to(dev), g.draft_tokens.to(dev)
+    bufs = [gl] + [gl.clone() for _ in range(ROTATE_ACCEPT - 1)]
+    nbytes = gl.numel() * 2
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    shapes = {}
+    for threads in (256, 512, 1024):
+        for loads in (4, 8, 16, 32):
+            def probe(i, t=threads, u=loads):
+                _lib.check(lib.bsx_read_probe(bufs[i % ROTATE_ACCEPT].data_ptr(), nbytes, t, u,
+                                              sink.data_ptr(), stream), "read_probe")
+            us = mean(time_events(probe, iters, 3))
+            shapes[f"{threads}x{loads}"] = round(us, 2)
+    best = min(shapes, key=shapes.get)
+    acc = mean(time_events(lambda i: bsx.evaluate_posterior(gd, bufs[i % ROTATE_ACCEPT],
+                                                            greedy=True, eos_token_id=-1),
+                           iters, 3))
+    ws = torch.empty(int(lib.bsx_argmax_ws_bytes(320, 128256)), dtype=torch.uint8, device=dev)
+    out = torch.empty(320, dtype=torch.int64, device=dev)
+    am = mean(time_events(lambda i: _lib.check(lib.bsx_argmax(
+        bufs[i % ROTATE_ACCEPT].data_ptr(), _lib.DTYPE_BF16, 320, 128256, 128256,
+        out.data_ptr(), ws.data_ptr(), ws.numel(), stream), "argmax"), iters, 3))
+    print(json.dumps({"calibration": "read", "bytes": nbytes, "rotating_buffers": ROTATE_ACCEPT,
+                      "probe_us_by_threads_x_loads": shapes, "best": best,
+                      "best_us": shapes[best],
+                      "best_GBs": round(nbytes / shapes[best] / 1e3, 1),
+                      "greedy_accept_us": round(acc, 2), "argmax_us": round(am, 2)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -601,6 +689,8 @@ def main() -> int:
     ap.add_argument("--only", choices=["attn2", "accept", "attn4", "attn3b", "attn3a"],
                     help="time one part alone (for rocprofv3 counter runs) and print its record")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--calibrate-read", action="store_true",
+                    help="time a one-pass read of the greedy logits in several launch shapes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the "
@@ -612,6 +702,8 @@ def main() -> int:
 
     if args.calibrate_copy:
         return calibrate_copy()
+    if args.calibrate_read:
+        return calibrate_read(args.steps)
 
     import batchspec_amd as bsx
     from batchspec_amd.workloads import config2

@@ -344,6 +344,25 @@ int bsx_page_table_update(int32_t* num_pages_d, int32_t* last_len_d, int32_t* ca
                           int page_size, int max_pages, int32_t* indptr_d,
                           int32_t* indices_d, int32_t* errors_d, void* stream);
 
+/* Greedy acceptance fused with the delete of the rejected tokens that follows it in the
+ * verify step: MTPEngine.evaluate_posterior's greedy branch
+ * (batchspec/backends/mtp_engine.py:553-560) and then PageTable.delete_kv(n_inserted -
+ * accept_nums) (batchspec/backends/base/page_table.py:95-137).  The arguments of
+ * bsx_accept_greedy (ids, or logits with the fused argmax and its workspace), then
+ * those of bsx_page_table_update for a delete of n_inserted - accept_b tokens per
+ * request (n_inserted >= k + 1: the tokens the step inserted).  One argmax launch (when
+ * given logits) plus one kernel that evaluates every request and updates the table;
+ * outputs and table state equal bsx_accept_greedy followed by bsx_page_table_update.
+ * At most 8192 requests. */
+int bsx_accept_greedy_delete(const int64_t* draft_d, const int64_t* target_ids_d,
+                             const void* target_logits_d, int dtype, int B, int k,
+                             int64_t vocab, int64_t eos_id, int mode, int64_t* bonus_d,
+                             int64_t* accept_d, uint8_t* eos_acc_d, void* ws_d,
+                             int64_t ws_bytes, int32_t n_inserted, int32_t* num_pages_d,
+                             int32_t* last_len_d, int32_t* cachelens_d, int page_size,
+                             int max_pages, int32_t* indptr_d, int32_t* indices_d,
+                             void* stream);
+
 /* Draft-tree masks on the device: replaces the MTP mask and position ids of
  * MTPEngine._setup_common_attn_mask_and_position_ids (batchspec/backends/mtp_engine.py:
  * 172-208) and the per-request ones/mask concatenation before plan() (:410-417), and
@@ -394,6 +413,14 @@ int64_t bsx_sample_ws_bytes(int64_t rows, int64_t vocab);
 int bsx_sample(const void* logits_d, int dtype, float temperature, int top_k, float top_p,
                const float* uniforms_d, int64_t rows, int64_t vocab, int32_t* out_d,
                void* ws_d, int64_t ws_bytes, void* stream);
+
+/* Streaming-read probe, a measurement kernel with no counterpart in the reference: reads
+ * `bytes` (a multiple of 16) from src_d once with non-temporal 16-byte loads, every load
+ * of a thread issued together, `threads` per workgroup and `loads_per_thread` loads per
+ * thread (1..32, powers of two); writes nothing but (rarely) a word of sink_d [1].  Its
+ * time is the floor of a kernel that reads the same bytes once. */
+int bsx_read_probe(const void* src_d, int64_t bytes, int threads, int loads_per_thread,
+                   uint32_t* sink_d, void* stream);
 
 #ifdef __cplusplus
 }

@@ -79,3 +79,69 @@ def test_noalloc_greedy_refuses_shapes_beyond_its_scratch():
     rc = lib.bsx_accept_greedy_noalloc(p, None, p, _lib.DTYPE_BF16, B, k, V, -1, 0, p, p, p, None)
     assert rc == _lib.BSX_ERR_CAPACITY
     assert b"allocation-free scratch" in lib.bsx_last_error()
+
+
+_CAPTURE_SCRIPT = r'''
+import sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+from batchspec_amd import _lib
+from batchspec_amd.workloads import greedy_case
+DEV = "cuda:0"
+lib = _lib.load()
+B, k, V = 64, 4, 128256
+c = greedy_case(B=B, k=k, V=V, seed=21, dtype=torch.bfloat16)
+draft = c.draft_tokens.to(DEV).contiguous()
+logits = c.target_logits.to(DEV).contiguous()
+outs = [torch.full((B,), -7, dtype=torch.int64, device=DEV) for _ in range(2)]
+eacc = torch.full((B,), 9, dtype=torch.uint8, device=DEV)
+
+def call(stream):
+    return lib.bsx_accept_greedy_noalloc(draft.data_ptr(), None, logits.data_ptr(),
+                                         _lib.DTYPE_BF16, B, k, V, -1, 0, outs[0].data_ptr(),
+                                         outs[1].data_ptr(), eacc.data_ptr(), stream)
+
+# the first call of the entry point in this process happens during the capture (its
+# per-device scratch address is looked up then)
+g = torch.cuda.CUDAGraph()
+s = torch.cuda.Stream()
+with torch.cuda.stream(s):
+    with torch.cuda.graph(g, stream=s):
+        rc = call(s.cuda_stream)
+assert rc == 0, lib.bsx_last_error()
+ws = torch.empty(int(lib.bsx_accept_greedy_ws_bytes(B, k, V)), dtype=torch.uint8, device=DEV)
+ref = [torch.empty(B, dtype=torch.int64, device=DEV) for _ in range(2)]
+ref_e = torch.empty(B, dtype=torch.uint8, device=DEV)
+st = torch.cuda.current_stream().cuda_stream
+_lib.check(lib.bsx_accept_greedy(draft.data_ptr(), None, logits.data_ptr(), _lib.DTYPE_BF16,
+                                 B, k, V, -1, 0, ref[0].data_ptr(), ref[1].data_ptr(),
+                                 ref_e.data_ptr(), ws.data_ptr(), ws.numel(), st), "greedy")
+torch.cuda.synchronize()
+for rep in range(4):
+    for t in outs:
+        t.fill_(-7)
+    eacc.fill_(9)
+    logits.mul_(1.0)  # eager work on the same stream between replays
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], ref[0]) and torch.equal(outs[1], ref[1]), rep
+    assert torch.equal(eacc, ref_e), rep
+print("capture ok", int(outs[1].sum()))
+'''
+
+
+def test_noalloc_greedy_captured_on_its_first_call():
+    """A fresh process whose first call of bsx_accept_greedy_noalloc is made while a
+    graph is being captured (the scratch address lookup included); four replays, with
+    eager work between them, each equal to bsx_accept_greedy with a workspace."""
+    import os
+    import subprocess
+    say("no-alloc greedy captured in a graph on its first call (fresh process)")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, root], capture_output=True,
+                       text=True, timeout=300)
+    say(r.stdout.strip()[-400:])
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "capture ok" in r.stdout
