@@ -68,7 +68,10 @@
 namespace bsx {
 namespace filt {
 
+using acc::load_group;
 using acc::load_one;
+using canon::kLanes;
+using canon::LaneState;
 using canon::fx40;
 using canon::kGroup;
 using canon::key_value;
@@ -1033,6 +1036,434 @@ __global__ void __launch_bounds__(kThreads) filter_deferred_kernel(RowsArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// Few rows: each row split over kParts workgroups (top-k on, top_k <= kDeferTopK).
+// ----------------------------------------------------------------------------
+// With one workgroup per row, a few hundred rows (the reference's default sampling at
+// the MTP verify shape: 320 rows of 128256) leave most compute units without work and
+// every row's pass latency-bound.  filter_parts_kernel gives each row kParts workgroups:
+// part p takes the canonical threads [64 p, 64 p + 64) (lanes [512 p, 512 p + 512), the
+// lanes 8t + i of canon.h), wave h of the part the lanes i = 2h, 2h + 1 of its 64
+// threads.  Every lane runs the canonical update of canon.h over its groups in order,
+// so the lane states are exactly those of the one-workgroup pass; they go to the
+// workspace, and filter_combine_kernel rescales them to the row max and sums them over
+// the same tree (row_stats' epilogue), giving the same (M, Z) bit for bit.
+// Candidates: part p's bound is the k-th largest of the maxima of its 512 first-round
+// groups (disjoint, so at least k of the part's elements reach it, and t* is at or above
+// the row's k-th largest element, which is at or above it); the part lists its elements
+// at or above the bound, keeps those at or above its own k-th largest listed key kb_p
+// (the part's k-th largest element) and writes them.  Every element of the row at or
+// above B = max_p kb_p is then written by its part, and t* >= the row's k-th largest
+// >= B, so the walk over the written keys at or above B finds t* and Z_K exactly.  A
+// part that cannot list (too many elements at its bound, a first round without k finite
+// maxima) sends the row to the exact threshold search of steps 3 and 4 in the combine
+// kernel.
+constexpr int kParts = 4;
+constexpr int kPartThreads = kThreads / kParts;  // canonical threads per part
+constexpr int kSplitMaxRows = 512;
+constexpr int64_t kSplitMinVocab = 8 * kLanes;  // every part has whole first-round groups
+constexpr int64_t kSplitMaxVocab = 16 * 8 * kLanes;  // at most 16 rounds: 32 hit bits
+constexpr int kSplitRounds = 2;                 // rounds per batch of loads (4, two batches in flight)
+constexpr int kPartList = kCap;                 // keys a part writes (about top_k + ties)
+static_assert(kThreads / 64 * 2 == 8, "a wave of a part holds two lanes of each thread");
+
+struct PartOut {
+  float m;        // maximum over the part's lanes (fmaxf-reduced)
+  uint32_t kb;    // the part's k-th largest listed key
+  int32_t count;  // keys written (>= kb), or -1: the part could not list
+  int32_t pad;
+};
+
+struct SplitArgs {
+  const void* a;  // rows [0, n_a)
+  int64_t n_a;
+  const void* b;  // rows [n_a, ...)
+  int64_t V;
+  float c;
+  int top_k;
+  float top_p;
+  RowInfo* info;
+  int32_t* lists;    // [rows][kCap]
+  float* lane_s;     // [rows][kLanes]
+  float* lane_r;     // [rows][kLanes]
+  PartOut* parts;    // [rows][kParts]
+  uint32_t* ckeys;   // [rows][kParts][kPartList]
+  int32_t* cidx;     // [rows][kParts][kPartList]
+};
+
+template <int DT>
+__device__ __forceinline__ const char* split_row(const SplitArgs& a, int64_t r) {
+  const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
+  return r < a.n_a ? static_cast<const char*>(a.a) + r * a.V * esz
+                   : static_cast<const char*>(a.b) + (r - a.n_a) * a.V * esz;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
+  __shared__ __align__(16) RowsLds L;
+  __shared__ float s_max[kThreads / 64];
+  constexpr int VW = DT == BSX_DTYPE_FP32 ? 2 : 1;
+  const int t = threadIdx.x;
+  // wave-uniform (scalar) so the lanes' group offsets below are scalar operands
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int64_t r = blockIdx.x / kParts;
+  const int p = (int)(blockIdx.x % kParts);
+  const int64_t V = a.V;
+  const char* row = split_row<DT>(a, r);
+  const float c = a.c;
+  const int k = a.top_k;
+  const int ct = p * kPartThreads + (t & 63);  // canonical thread
+  const int i0 = 2 * wave;                     // its lanes i0, i0 + 1
+  const int64_t G = ceil_div(V, (int64_t)kGroup);
+  const int64_t G_whole = V / kGroup;
+  const __amdgpu_buffer_rsrc_t rsrc = row_rsrc(row, V * (int64_t)(VW == 2 ? 4 : 2));
+  LaneState st[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    st[e].m = -INFINITY;
+    st[e].s = 0.f;
+    st[e].r = canon::kRefStart;
+  }
+  if (t == 0) L.count = 0;
+  float lf = INFINITY;
+  uint32_t hits = 0u;  // bit 2 j + e: group ct + 256 (8 j + i0 + e) reached the bound
+
+  // Loads of the groups of rounds [cq, cq + 8 NR) of this thread's two lanes; a load past
+  // the row returns 0 (buffer range), and groups past G_whole are not used from it.
+  auto load_rounds = [&](int64_t cq, auto& w, auto nr_tag) {
+    constexpr int NR = decltype(nr_tag)::value;
+#pragma unroll
+    for (int q = 0; q < NR; ++q)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int h = 0; h < VW; ++h)
+          w[q][e][h] = load_nt_b128(rsrc, (ct * VW + h) * 16,
+                                    (int)(cq + 8 * q + i0 + e) * 4096 * VW);
+  };
+  auto unpack = [&](const u32x4 (&wv)[VW], float (&x)[8]) {
+    if constexpr (DT == BSX_DTYPE_FP32) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        x[u] = __uint_as_float(wv[0][u]);
+        x[4 + u] = __uint_as_float(wv[1][u]);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        x[2 * u] = lo_f32<DT>(wv[0][u]);
+        x[2 * u + 1] = hi_f32<DT>(wv[0][u]);
+      }
+    }
+  };
+  auto max8f = [](const float (&x)[8]) {
+    return __builtin_elementwise_maximum(
+        __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[0], x[1]),
+                                      __builtin_elementwise_maximum(x[2], x[3])),
+        __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[4], x[5]),
+                                      __builtin_elementwise_maximum(x[6], x[7])));
+  };
+  // One round cq of the two lanes, with the arithmetic of row_stats: a round whole for
+  // the canonical thread (all 8 of its groups complete) by the whole-round path, the
+  // other rounds group by group.
+  auto do_round = [&](int64_t cq, const u32x4 (&wr)[2][VW], const float (&gm)[2],
+                      const float (&x)[2][8]) {
+    const bool whole_round = (int64_t)ct + 256 * (cq + 7) < G_whole;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int64_t g = (int64_t)ct + 256 * (cq + i0 + e);
+      if (g < G_whole && !whole_round) {
+        float gmf = x[e][0];
+#pragma unroll
+        for (int u = 1; u < 8; ++u) gmf = fmaxf(gmf, x[e][u]);
+        canon::lane_update(st[e], x[e], 8, gmf, c);
+        if (gmf >= lf) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (x[e][u] >= lf) push_candidate(L, x[e][u], g * kGroup + u);
+        }
+      } else if (g < G_whole) {
+        const float rr = canon::lane_reference(st[e], gm[e], c);
+        // = 0 + w0 + ... exactly: weights are >= +0
+        float gs = canon::weight(x[e][0], c, -rr);
+#pragma unroll
+        for (int u = 1; u < 8; ++u) gs = gs + canon::weight(x[e][u], c, -rr);
+        st[e].s = st[e].s + gs;
+        hits |= (gm[e] >= lf ? 1u : 0u) << (2 * (int)(cq >> 3) + e);
+      } else if (g < G) {
+        float xp[8];
+        const int n = load_group<DT>(row, g, V, true, xp);
+        float gmp = xp[0];
+#pragma unroll
+        for (int u = 1; u < 8; ++u)
+          if (u < n) gmp = fmaxf(gmp, xp[u]);
+        canon::lane_update(st[e], xp, n, gmp, c);
+        if (gmp >= lf) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (u < n && xp[u] >= lf) push_candidate(L, xp[u], g * kGroup + u);
+        }
+      }
+    }
+  };
+
+  // Round 0 on its own (the vocabulary is at least kSplitMinVocab, so all its groups are
+  // whole): the part's bound is the k-th largest of its 512 first-round group maxima
+  // (every thread calls the selection; -inf values are not counted).
+  {
+    u32x4 w[1][2][VW];
+    load_rounds(0, w, std::integral_constant<int, 1>());
+    float x[2][8], gm[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      unpack(w[0][e], x[e]);
+      gm[e] = max8f(x[e]);
+    }
+    const uint32_t kb = kth_key_call(L, gm[0], gm[1], -INFINITY, -INFINITY, -INFINITY,
+                                     -INFINITY, -INFINITY, -INFINITY, k);
+    lf = kb == 0u ? INFINITY : key_value(kb);
+    if (t == 0 && kb == 0u) L.count = kCands + 1;  // cannot list: the combine searches
+    do_round(0, w[0], gm, x);
+  }
+  // The following rounds that are whole for every thread of the part run in batches of
+  // kSplitRounds, software-pipelined over two register sets: each batch's loads go out
+  // before the previous batch is computed, so a wave's arithmetic overlaps its own loads
+  // (the workgroups of all rows start together and would otherwise alternate between
+  // loading and computing in step).  That loop holds only the whole-round arithmetic;
+  // the rounds after it (at most a few) take do_round's per-group rules.
+  constexpr int NR = kSplitRounds;
+  const std::integral_constant<int, NR> nr;
+  auto compute_whole = [&](int64_t cq0, const u32x4 (&w)[NR][2][VW]) {
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        float x[8];
+        unpack(w[q][e], x);
+        const float gm = max8f(x);
+        const float rr = canon::lane_reference(st[e], gm, c);
+        float gs = canon::weight(x[0], c, -rr);
+#pragma unroll
+        for (int u = 1; u < 8; ++u) gs = gs + canon::weight(x[u], c, -rr);
+        st[e].s = st[e].s + gs;
+        hits |= (gm >= lf ? 1u : 0u) << (2 * (int)((cq0 + 8 * q) >> 3) + e);
+      }
+    }
+  };
+  // rounds [8, c_whole) are whole for every thread of the part (its largest canonical
+  // thread is the binding one), in whole batches
+  const int64_t ct_max = (int64_t)p * kPartThreads + kPartThreads - 1;
+  const int64_t n_whole = G_whole > ct_max + 256 * 7 ? (G_whole - 1 - ct_max - 256 * 7) / 2048 + 1 : 0;
+  const int64_t c_whole = 8 + ((n_whole - 1) / NR) * NR * 8;  // end of the batched rounds
+  int64_t c0 = 8;
+  if (c_whole > 8) {
+    u32x4 wa[NR][2][VW], wb[NR][2][VW];
+    load_rounds(8, wa, nr);
+    for (;;) {
+      const bool more_b = c0 + 8 * NR < c_whole;
+      if (more_b) load_rounds(c0 + 8 * NR, wb, nr);
+      compute_whole(c0, wa);
+      c0 += 8 * NR;
+      if (!more_b) break;
+      const bool more_a = c0 + 8 * NR < c_whole;
+      if (more_a) load_rounds(c0 + 8 * NR, wa, nr);
+      compute_whole(c0, wb);
+      c0 += 8 * NR;
+      if (!more_a) break;
+    }
+  }
+  for (; (int64_t)ct + 256 * c0 < G; c0 += 8) {
+    u32x4 w[1][2][VW];
+    load_rounds(c0, w, std::integral_constant<int, 1>());
+    float x[2][8], gm[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      unpack(w[0][e], x[e]);
+      gm[e] = max8f(x[e]);
+    }
+    do_round(c0, w[0], gm, x);
+  }
+  // lane states and the part's maximum
+  float* ls = a.lane_s + r * kLanes;
+  float* lr = a.lane_r + r * kLanes;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    ls[8 * ct + i0 + e] = st[e].s;
+    lr[8 * ct + i0 + e] = st[e].r;
+  }
+  float mx = fmaxf(st[0].m, st[1].m);
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  if ((t & 63) == 0) s_max[wave] = mx;
+  // The groups that reached the bound (a few hundred per part) are listed in LDS and
+  // read again one per thread: a single round trip, where a thread reading its own noted
+  // groups in turn would put several dependent ones on the workgroup's tail.
+  if (t == 0) L.ng = 0;
+  __syncthreads();
+  uint32_t hb = hits;
+#pragma unroll 1
+  while (hb != 0u) {
+    const int bit = __builtin_ctz(hb);
+    hb &= hb - 1u;
+    const int slot = atomicAdd(&L.ng, 1);
+    if (slot < kBins) L.hist[slot] = (uint32_t)(ct + 256 * (8 * (bit >> 1) + i0 + (bit & 1)));
+  }
+  __syncthreads();
+  const int ng = min(L.ng, kBins);
+  for (int q = t; q < ng; q += kThreads) {
+    const int64_t g = L.hist[q];
+    float xg[8];
+    load8<DT>(row, g, xg);
+    uint32_t hm = 0u;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) hm |= (xg[u] >= lf ? 1u : 0u) << u;
+#pragma unroll 1
+    while (hm != 0u) {
+      const int u = __builtin_ctz(hm);
+      hm &= hm - 1u;
+      // the element again from cache: indexing xg by a run-time u would put it in
+      // scratch memory
+      push_candidate(L, load_one<DT>(row, g * kGroup + u), g * kGroup + u);
+    }
+  }
+  __syncthreads();
+  if (L.ng > kBins && t == 0) L.count = kCands + 1;  // could not note them all
+  __syncthreads();
+  const int n = L.count;
+  PartOut po;
+  po.m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  po.kb = 0u;
+  po.count = -1;
+  po.pad = 0;
+  if (n <= kCands) {
+    // keep the keys at or above the part's k-th largest listed key (its k-th largest
+    // element: every element at or above the bound is listed)
+    constexpr int PER = kCands / kThreads;
+    uint32_t ck[PER];
+    int32_t ci[PER];
+    float cv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cv[j] = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int s = t + kThreads * j;
+      ck[j] = s < n ? L.ckey[s] : 0u;
+      ci[j] = s < n ? L.cidx[s] : 0;
+      if (s < n) cv[j] = key_value(ck[j]);
+    }
+    const uint32_t kb =
+        kth_key_call(L, cv[0], cv[1], cv[2], cv[3], cv[4], cv[5], cv[6], cv[7], k);
+    if (t == 0) L.nk = 0;
+    __syncthreads();
+    uint32_t* okeys = a.ckeys + (r * kParts + p) * kPartList;
+    int32_t* oidx = a.cidx + (r * kParts + p) * kPartList;
+    if (kb != 0u) {
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (t + kThreads * j < n && ck[j] >= kb) {
+          const int slot = atomicAdd(&L.nk, 1);
+          if (slot < kPartList) {
+            okeys[slot] = ck[j];
+            oidx[slot] = ci[j];
+          }
+        }
+    }
+    __syncthreads();
+    if (kb != 0u && L.nk <= kPartList) {
+      po.kb = kb;
+      po.count = L.nk;
+    }
+  }
+  if (t == 0) a.parts[r * kParts + p] = po;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) filter_combine_kernel(SplitArgs a) {
+  __shared__ __align__(16) RowsLds L;
+  __shared__ float wave_val[kThreads / 64];
+  const int t = threadIdx.x;
+  const int64_t r = blockIdx.x;
+  const int64_t V = a.V;
+  const char* row = split_row<DT>(a, r);
+  const float c = a.c;
+  const bool use_k = a.top_k > 0 && (int64_t)a.top_k < V;
+  const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
+  // Every load of the row's records goes out at once: the part records, the lane states
+  // and all kParts * kPartList key slots of the parts (masked by their counts below).
+  PartOut po[kParts];
+#pragma unroll
+  for (int q = 0; q < kParts; ++q) po[q] = a.parts[r * kParts + q];
+  constexpr int SL = kParts * kPartList / kThreads;
+  static_assert(kParts * kPartList % kThreads == 0, "key slots split evenly over threads");
+  uint32_t sk[SL];
+  int32_t si[SL];
+#pragma unroll
+  for (int j = 0; j < SL; ++j) {
+    const int64_t slot = r * kParts * kPartList + t + kThreads * j;
+    sk[j] = a.ckeys[slot];
+    si[j] = a.cidx[slot];
+  }
+  // (M, Z): row_stats' epilogue on the lane states of the parts
+  float mx = po[0].m;
+#pragma unroll
+  for (int q = 1; q < kParts; ++q) mx = fmaxf(mx, po[q].m);
+  const float rho_m = mx * c;
+  const f32x4* ls4 = reinterpret_cast<const f32x4*>(a.lane_s + r * kLanes + 8 * t);
+  const f32x4* lr4 = reinterpret_cast<const f32x4*>(a.lane_r + r * kLanes + 8 * t);
+  const f32x4 s0 = ls4[0], s1 = ls4[1], r0 = lr4[0], r1 = lr4[1];
+  const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  const float rv[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+  float rs[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) rs[i] = canon::lane_rescaled(LaneState{-INFINITY, sv[i], rv[i]}, rho_m);
+  float sum = ((rs[0] + rs[1]) + (rs[2] + rs[3])) + ((rs[4] + rs[5]) + (rs[6] + rs[7]));
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) sum = sum + __shfl_xor(sum, m);
+  if ((t & 63) == 0) wave_val[t >> 6] = sum;
+  if (t == 0) L.count = 0;
+  __syncthreads();
+  const float M = mx;
+  const float Z = (wave_val[0] + wave_val[1]) + (wave_val[2] + wave_val[3]);
+  const float neg = -(M * c);
+  const uint64_t target = use_p ? (uint64_t)ceilf((a.top_p * Z) * 0x1p40f) : 0ull;
+
+  bool listed = false;
+  bool can = true;
+  uint32_t bkey = 0u;
+#pragma unroll
+  for (int q = 0; q < kParts; ++q) {
+    can = can && po[q].count >= 0;
+    bkey = max(bkey, po[q].kb);
+  }
+  if (can) {
+    // the written keys at or above B = max kb_p: every element of the row there
+#pragma unroll
+    for (int j = 0; j < SL; ++j) {
+      const int slot = t + kThreads * j;
+      const int q = slot / kPartList;
+      int cnt = po[0].count;
+#pragma unroll
+      for (int qq = 1; qq < kParts; ++qq) cnt = q == qq ? po[qq].count : cnt;
+      if (slot - q * kPartList < cnt && sk[j] >= bkey) {
+        const int at = atomicAdd(&L.count, 1);
+        if (at < kCands) {
+          L.ckey[at] = sk[j];
+          L.cidx[at] = si[j];
+        }
+      }
+    }
+    __syncthreads();
+    const int n = L.count;
+    if (n <= kCands) listed = walk(L, n, c, neg, use_k, use_p, a.top_k, target, a.lists + r * kCap);
+  }
+  if (!listed) {
+    const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
+    const bool vec = ((V * esz) % 16 == 0) && (((uintptr_t)row) % 16 == 0);
+    large_threshold<DT>(L, row, V, vec, c, neg, use_k, use_p, a.top_k, target);
+  }
+  write_info(L, a.info + r, M);
+}
+
+// ----------------------------------------------------------------------------
 // Acceptance and draws over filtered rows.
 // ----------------------------------------------------------------------------
 struct ChainArgs {
@@ -1046,6 +1477,8 @@ struct ChainArgs {
   int64_t V;
   float c;
   uint64_t* tiles;   // [B][2][draw_tiles(V)] tile sums of the whole-row draws
+  int tiles_ready;   // filter_tiles_kernel ran (else a row without a list sums its tiles
+                     // in filter_chain_kernel)
   int32_t* out_ids;  // [B, k+1]
   int32_t* accepted;
   int32_t* emitted;
@@ -1268,6 +1701,7 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
   __shared__ uint64_t excl[kThreads];
   __shared__ uint64_t s_wave[kThreads / 64];
   __shared__ uint64_t tsum[kMaxTiles];
+  __shared__ uint64_t tloc[2][kMaxTiles];  // tile sums made here (tiles_ready == 0)
   const int b = blockIdx.x;
   const int t = threadIdx.x;
   const int k = a.k;
@@ -1323,12 +1757,38 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
     const int ntiles = draw_tiles(V);
     const uint64_t* ts = a.tiles + (int64_t)b * 2 * ntiles;
     const int wave = t >> 6, lane = t & 63;
+    if (!a.tiles_ready) {
+      // the tile sums of filter_tiles_kernel, here (it was not launched: with a small
+      // top_k every row is expected to list, and a row that does not is rare); each wave
+      // sums 8 of its tiles per round, their loads together
+      constexpr int U = 8;
+      for (int T0 = wave; T0 < ntiles; T0 += (kThreads / 64) * U) {
+        uint64_t sq[U], sp[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int T = T0 + (kThreads / 64) * u;
+          R.sums((int64_t)(T < ntiles ? T : 0) * tile + (int64_t)lane * E, E, sq[u], sp[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int T = T0 + (kThreads / 64) * u;
+          const uint64_t q = has_q ? wave_sum_u64(sq[u]) : 0ull;
+          const uint64_t pp = wave_sum_u64(sp[u]);
+          if (lane == 0 && T < ntiles) {
+            tloc[0][T] = q;
+            tloc[1][T] = pp;
+          }
+        }
+      }
+      __syncthreads();
+    }
     uint64_t total = 0ull;
     bool with_q = has_q;
     for (int pass = 0; pass < 2; ++pass) {
       with_q = has_q && pass == 0;
       if (pass == 1 && !has_q) break;
-      for (int T = t; T < ntiles; T += kThreads) tsum[T] = ts[(with_q ? 0 : ntiles) + T];
+      for (int T = t; T < ntiles; T += kThreads)
+        tsum[T] = a.tiles_ready ? ts[(with_q ? 0 : ntiles) + T] : tloc[with_q ? 0 : 1][T];
       __syncthreads();
       // thread t: tiles [8t, 8t + 8); exclusive prefix of those groups
       uint64_t mine = 0ull;
@@ -1444,9 +1904,23 @@ static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 using namespace bsx;
 
-extern "C" int64_t bsx_filter_ws_bytes(int64_t rows) {
+// Workspace of the split rows (few rows): lane states, part records, part lists.
+// Non-decreasing in rows (a caller sizing for more rows always has room for the split
+// region of fewer), so sized for kSplitMaxRows above it.
+static int64_t split_ws_bytes(int64_t rows) {
+  rows = std::min<int64_t>(rows, filt::kSplitMaxRows);
+  return 2 * filt::align256(rows * canon::kLanes * 4) +
+         filt::align256(rows * filt::kParts * (int64_t)sizeof(filt::PartOut)) +
+         2 * filt::align256(rows * filt::kParts * filt::kPartList * 4);
+}
+
+static int64_t rows_ws_bytes(int64_t rows) {
   return filt::align256(rows * (int64_t)sizeof(filt::RowInfo)) +
          filt::align256(rows * filt::kCap * 4);
+}
+
+extern "C" int64_t bsx_filter_ws_bytes(int64_t rows) {
+  return rows_ws_bytes(rows) + split_ws_bytes(rows);
 }
 
 static bool filters_on(int top_k, float top_p, int64_t vocab) {
@@ -1473,6 +1947,41 @@ static int launch_filter_rows(const void* a, int64_t n_a, const void* b, int64_t
   const bool use_k = top_k > 0 && (int64_t)top_k < V;
   const bool use_p = top_p > 0.f && top_p < 1.f;
   ra.defer = (use_p && !use_k) || (use_k && top_k > filt::kDeferTopK);
+  const int64_t rows = n_a + n_b;
+  const int64_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
+  const bool aligned = (V * esz) % 16 == 0 && (uintptr_t)a % 16 == 0 &&
+                       (b == nullptr || (uintptr_t)b % 16 == 0);
+  if (use_k && top_k <= filt::kDeferTopK && rows <= filt::kSplitMaxRows &&
+      V >= filt::kSplitMinVocab && V <= filt::kSplitMaxVocab && aligned) {
+    // few rows: each row over kParts workgroups, then one combine per row
+    filt::SplitArgs sa;
+    sa.a = a;
+    sa.n_a = n_a;
+    sa.b = b;
+    sa.V = V;
+    sa.c = c;
+    sa.top_k = top_k;
+    sa.top_p = top_p;
+    sa.info = ra.info;
+    sa.lists = ra.lists;
+    char* base = static_cast<char*>(ws) + rows_ws_bytes(rows);
+    sa.lane_s = reinterpret_cast<float*>(base);
+    base += filt::align256(rows * canon::kLanes * 4);
+    sa.lane_r = reinterpret_cast<float*>(base);
+    base += filt::align256(rows * canon::kLanes * 4);
+    sa.parts = reinterpret_cast<filt::PartOut*>(base);
+    base += filt::align256(rows * filt::kParts * (int64_t)sizeof(filt::PartOut));
+    sa.ckeys = reinterpret_cast<uint32_t*>(base);
+    base += filt::align256(rows * filt::kParts * filt::kPartList * 4);
+    sa.cidx = reinterpret_cast<int32_t*>(base);
+    hipLaunchKernelGGL((filt::filter_parts_kernel<DT>), dim3((unsigned)(rows * filt::kParts)),
+                       dim3(filt::kThreads), 0, st, sa);
+    BSX_LAUNCH_CHECK();
+    hipLaunchKernelGGL((filt::filter_combine_kernel<DT>), dim3((unsigned)rows),
+                       dim3(filt::kThreads), 0, st, sa);
+    BSX_LAUNCH_CHECK();
+    return BSX_OK;
+  }
   hipLaunchKernelGGL((filt::filter_rows_kernel<DT>), dim3((unsigned)(n_a + n_b)),
                      dim3(filt::kThreads), 0, st, ra);
   BSX_LAUNCH_CHECK();
@@ -1492,10 +2001,17 @@ static int filtered_chain_impl(filt::ChainArgs& ca, void* ws, hipStream_t st, in
   int rc = launch_filter_rows<DT>(ca.t_logits, n_t, ca.d_logits, n_d, ca.V, ca.c, top_k, top_p,
                                   ws, st);
   if (rc != BSX_OK) return rc;
-  const int parts = (int)ceil_div(filt::draw_tiles(ca.V), filt::kTilesPerPart);
-  hipLaunchKernelGGL((filt::filter_tiles_kernel<DT>), dim3((unsigned)ca.B, (unsigned)parts),
-                     dim3(filt::kThreads), 0, st, ca);
-  BSX_LAUNCH_CHECK();
+  // With a small top_k every row is expected to list its kept set: the chain kernel sums
+  // the tiles itself for the rare row that does not (ties), and the tile-sum launch is
+  // left out.  Otherwise (top-p alone, a large top_k) the tile sums come first.
+  const bool use_k = top_k > 0 && (int64_t)top_k < ca.V;
+  ca.tiles_ready = !(use_k && top_k <= filt::kDeferTopK);
+  if (ca.tiles_ready) {
+    const int parts = (int)ceil_div(filt::draw_tiles(ca.V), filt::kTilesPerPart);
+    hipLaunchKernelGGL((filt::filter_tiles_kernel<DT>), dim3((unsigned)ca.B, (unsigned)parts),
+                       dim3(filt::kThreads), 0, st, ca);
+    BSX_LAUNCH_CHECK();
+  }
   hipLaunchKernelGGL((filt::filter_chain_kernel<DT>), dim3((unsigned)ca.B), dim3(filt::kThreads),
                      0, st, ca);
   BSX_LAUNCH_CHECK();

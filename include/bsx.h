@@ -284,7 +284,7 @@ int bsx_accept_greedy(const int64_t* draft_d, const int64_t* target_ids_d,
  * bsx_accept_greedy without ws_d / ws_bytes: the argmax partials go to a file-scope
  * device array of BSX_NOALLOC_SCRATCH_BYTES bytes per GPU, held until the process
  * ends.  Shapes whose partials exceed it (bsx_accept_greedy_ws_bytes(B, k, vocab) >
- * BSX_NOALLOC_SCRATCH_BYTES; at vocab 128256 in bf16 that is B*(k+1) > 131072 rows)
+ * BSX_NOALLOC_SCRATCH_BYTES; at vocab 128256 in bf16 that is B*(k+1) > 32768 rows)
  * return BSX_ERR_CAPACITY.  The library allocates nothing here.  Every call on a GPU
  * shares that GPU's array: calls that overlap in time on one GPU race. */
 #define BSX_NOALLOC_SCRATCH_BYTES (4 << 20)
