@@ -1090,6 +1090,64 @@ struct SplitArgs {
   int32_t* cidx;     // [rows][kParts][kPartList]
 };
 
+// A lower bound of the k-th largest of the keys (N per thread, 0 = no value), from a
+// 256-bin histogram of their distance to the largest key at bf16 resolution (key >> 16):
+// the lower edge of the first bin, from the top, at which k keys are reached.  At least
+// k of the keys are at or above it, and it is within one bf16 step of the k-th largest.
+// Returns 0 when the k largest do not fit the 256 bins (or there are fewer than k).
+// Every thread calls it; uses hist, part and bin of L.
+template <int N>
+__device__ __noinline__ uint32_t fine_bound(RowsLds& L, const uint32_t (&key)[N], int k) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  uint32_t kmax = 0u;
+#pragma unroll
+  for (int i = 0; i < N; ++i) kmax = max(kmax, key[i]);
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, m));
+  if (lane == 0) L.part[wave] = kmax;
+  L.hist[t] = 0u;
+  __syncthreads();
+  kmax = max(max(L.part[0], L.part[1]), max(L.part[2], L.part[3]));
+  const uint32_t top = kmax >> 16;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const uint32_t d = top - (key[i] >> 16);
+    if (key[i] != 0u && d < 256u) atomicAdd(&L.hist[d], 1u);
+  }
+  __syncthreads();
+  if (t < 64) {
+    const u32x4 c = reinterpret_cast<const u32x4*>(L.hist)[t];
+    const uint32_t s = (c[0] + c[1]) + (c[2] + c[3]);
+    uint32_t incl = s;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_up((int)incl, d);
+      if (lane >= d) incl += o;
+    }
+    const uint64_t reach = __builtin_amdgcn_ballot_w64(k <= 1024 && incl >= (uint32_t)k);
+    int bin = -1;
+    if (reach != 0ull) {
+      const int ls = __builtin_ctzll(reach);  // first lane (from the top) reaching k
+      uint32_t cum = (uint32_t)__shfl((int)(incl - s), ls);
+      const u32x4 cl = reinterpret_cast<const u32x4*>(L.hist)[ls];
+      bool found = false;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        cum += cl[q];
+        if (!found && cum >= (uint32_t)k) {
+          bin = 4 * ls + q;
+          found = true;
+        }
+      }
+    }
+    if (t == 0) L.bin = kmax == 0u ? -1 : bin;
+  }
+  __syncthreads();
+  const int bin = L.bin;
+  __syncthreads();
+  return bin < 0 ? 0u : (top - (uint32_t)bin) << 16;
+}
+
 template <int DT>
 __device__ __forceinline__ const char* split_row(const SplitArgs& a, int64_t r) {
   const size_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
@@ -1218,8 +1276,17 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
       unpack(w[0][e], x[e]);
       gm[e] = max8f(x[e]);
     }
-    const uint32_t kb = kth_key_call(L, gm[0], gm[1], -INFINITY, -INFINITY, -INFINITY,
-                                     -INFINITY, -INFINITY, -INFINITY, k);
+    // (-inf and negative NaN images are left out, as kth_key does)
+    uint32_t gk[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      gk[e] = okey(gm[e]);
+      if ((gk[e] >> kBinShift) < (uint32_t)kFirstFiniteBin) gk[e] = 0u;
+    }
+    uint32_t kb = fine_bound<2>(L, gk, k);
+    if (kb == 0u)  // the k largest spread over more than 256 bf16 steps
+      kb = kth_key_call(L, gm[0], gm[1], -INFINITY, -INFINITY, -INFINITY, -INFINITY, -INFINITY,
+                        -INFINITY, k);
     lf = kb == 0u ? INFINITY : key_value(kb);
     if (t == 0 && kb == 0u) L.count = kCands + 1;  // cannot list: the combine searches
     do_round(0, w[0], gm, x);
@@ -1350,8 +1417,12 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
       ci[j] = s < n ? L.cidx[s] : 0;
       if (s < n) cv[j] = key_value(ck[j]);
     }
-    const uint32_t kb =
-        kth_key_call(L, cv[0], cv[1], cv[2], cv[3], cv[4], cv[5], cv[6], cv[7], k);
+    uint32_t lk[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) lk[j] = t + kThreads * j < n ? ck[j] : 0u;
+    uint32_t kb = fine_bound<PER>(L, lk, k);
+    if (kb == 0u)
+      kb = kth_key_call(L, cv[0], cv[1], cv[2], cv[3], cv[4], cv[5], cv[6], cv[7], k);
     if (t == 0) L.nk = 0;
     __syncthreads();
     uint32_t* okeys = a.ckeys + (r * kParts + p) * kPartList;
