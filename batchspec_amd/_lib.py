@@ -89,6 +89,8 @@ SIGNATURES = {
     "bsx_attn_plan_device": (c_int, [POINTER(AttnPlan), _P, _P, _P, c_int64, _P, _P]),
     "bsx_attn_run": (c_int, [POINTER(AttnPlan), _P, _P, c_int, _P, c_int64, _P, _P, c_int64, _P,
                              _P, _P, c_int64, _P, _P]),
+    "bsx_attn_run_append": (c_int, [POINTER(AttnPlan), _P, _P, c_int, _P, c_int64, _P, _P, c_int64,
+                                    _P, _P, _P, c_int64, _P, _P, c_int64, _P, c_int64, _P]),
     "bsx_get_seq_lens": (c_int, [_P, _P, c_int, c_int, _P, _P]),
     "bsx_get_batch_indices_positions": (c_int, [_P, _P, c_int, c_int, _P, _P, _P]),
     "bsx_append_paged_kv_cache": (c_int, [_P, _P, c_int64, c_int64, _P, _P, c_int, _P, _P, c_int64,

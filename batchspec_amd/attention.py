@@ -456,8 +456,18 @@ class BatchPrefillWithPagedKVCacheWrapper:
     def run(self, q: torch.Tensor,
             paged_kv_cache: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]],
             out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
-            return_lse: bool = False, **unused):
-        """Attention output [nnz, num_qo_heads, head_dim] (and lse [nnz, num_qo_heads])."""
+            return_lse: bool = False, *, append_key: Optional[torch.Tensor] = None,
+            append_value: Optional[torch.Tensor] = None, **unused):
+        """Attention output [nnz, num_qo_heads, head_dim] (and lse [nnz, num_qo_heads]).
+
+        With ``append_key`` / ``append_value`` ([nnz, num_kv_heads, head_dim], the cache's
+        dtype) the layer's KV update runs in the same call: the rows go to the last qo_len
+        positions of each request (StandardKVCache.update with kv_append_indptr =
+        qo_indptr, batchspec/models/modules/kv_cache.py:47-84, as
+        batchspec/models/modules/attention/standard.py:63-66 calls it) and attention sees
+        them, as the update followed by run() does.  The plan's page table must already
+        count those tokens (insert_kv runs before the layers).  Fused into the attention
+        launch for the per-wave kernel with pages of at least 16 tokens."""
         plan = self._plan
         if plan is None:
             raise RuntimeError("plan() must be called before run()")
@@ -489,14 +499,26 @@ class BatchPrefillWithPagedKVCacheWrapper:
         blob = ws[: int(plan.plan_ints) * 4]
         fws = ws[self._blob_bytes:] if int(plan.float_ws_bytes) > 0 else None
         lib = _lib.load()
-        rc = lib.bsx_attn_run(ctypes.byref(plan), blob.data_ptr(),
-                              None if fws is None else fws.data_ptr(),
-                              dtype_code(q.dtype), q.data_ptr(), q.stride(0),
-                              k_cache.data_ptr(), v_cache.data_ptr(), page_stride,
-                              self._kv_indices.data_ptr(),
-                              None if self._mask_words is None or plan.mask_mode != _lib.MASK_TREE
-                              else self._mask_words.data_ptr(),
-                              out.data_ptr(), out.stride(0), _lib.ptr(lse), stream_of(dev))
+        mw = (None if self._mask_words is None or plan.mask_mode != _lib.MASK_TREE
+              else self._mask_words.data_ptr())
+        if append_key is None and append_value is None:
+            rc = lib.bsx_attn_run(ctypes.byref(plan), blob.data_ptr(),
+                                  None if fws is None else fws.data_ptr(),
+                                  dtype_code(q.dtype), q.data_ptr(), q.stride(0),
+                                  k_cache.data_ptr(), v_cache.data_ptr(), page_stride,
+                                  self._kv_indices.data_ptr(), mw,
+                                  out.data_ptr(), out.stride(0), _lib.ptr(lse), stream_of(dev))
+        else:
+            kn = _append_rows(append_key, "append_key", q, plan, k_cache.dtype)
+            vn = _append_rows(append_value, "append_value", q, plan, k_cache.dtype)
+            rc = lib.bsx_attn_run_append(ctypes.byref(plan), blob.data_ptr(),
+                                         None if fws is None else fws.data_ptr(),
+                                         dtype_code(q.dtype), q.data_ptr(), q.stride(0),
+                                         k_cache.data_ptr(), v_cache.data_ptr(), page_stride,
+                                         self._kv_indices.data_ptr(), mw,
+                                         out.data_ptr(), out.stride(0), _lib.ptr(lse),
+                                         kn.data_ptr(), kn.stride(0), vn.data_ptr(), vn.stride(0),
+                                         stream_of(dev))
         _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.run")
         if torch.cuda.is_current_stream_capturing():
             self._captured_sig = self._launch_sig(plan, self._blob_bytes)
@@ -511,6 +533,22 @@ class BatchPrefillWithPagedKVCacheWrapper:
     @property
     def plan_info(self) -> Optional[_lib.AttnPlan]:
         return self._plan
+
+
+def _append_rows(x: Optional[torch.Tensor], name: str, q: torch.Tensor, plan,
+                 dtype: torch.dtype) -> torch.Tensor:
+    """The appended K or V rows: [q rows, num_kv_heads, head_dim], dense heads, the
+    cache's dtype, on q's device."""
+    if x is None:
+        raise ValueError("append_key and append_value go together")
+    shape = (q.shape[0], plan.num_kv_heads, plan.head_dim)
+    if tuple(x.shape) != shape or x.dtype != dtype or x.device != q.device:
+        raise ValueError(f"{name} must be {list(shape)} {dtype} on {q.device}, got "
+                         f"{list(x.shape)} {x.dtype} on {x.device}")
+    if x.stride(2) != 1 or x.stride(1) != plan.head_dim or x.stride(0) % 8 != 0 \
+            or x.data_ptr() % 16 != 0:
+        x = x.contiguous()
+    return x
 
 
 def _as_dtype(d) -> torch.dtype:

@@ -18,7 +18,9 @@ see an opaque operator with known output shapes:
   per name) and binds it to a ``BatchPrefillWithPagedKVCacheWrapper``; the op runs that
   wrapper's current plan, so ``plan()`` stays outside the compiled region, as in the
   reference (the engines plan before calling the compiled forward).  Binding another
-  wrapper to the same name later re-targets the op without recompiling.
+  wrapper to the same name later re-targets the op without recompiling.  It also defines
+  ``torch.ops.bsx.<name>_with_append(q, k, v, kv_cache)``, the layer's update and
+  attention in one call (the append fused into the attention launch).
 * ``torch.ops.bsx.update_kv(...)``: the fused paged append, mutating ``kv_cache`` in place.
 * ``torch.ops.bsx.evaluate_posterior_greedy`` / ``evaluate_posterior_sampling``: the
   acceptance of batchspec/backends/mtp_engine.py:533-575 with its output tuple.
@@ -54,13 +56,32 @@ def _attention_op(name: str):
     return op
 
 
+def _attention_append_op(name: str):
+    @torch.library.custom_op(f"bsx::{name}_with_append", mutates_args=("kv_cache",))
+    def op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+           kv_cache: torch.Tensor) -> torch.Tensor:
+        w = _WRAPPERS.get(name)
+        if w is None:
+            raise RuntimeError(f"torch.ops.bsx.{name}_with_append: no wrapper bound")
+        return w.run(q, kv_cache, append_key=k, append_value=v)
+
+    @op.register_fake
+    def _(q, k, v, kv_cache):
+        return torch.empty_like(q)
+
+    return op
+
+
 def bind_attention(name: str, wrapper) -> object:
     """``torch.ops.bsx.<name>(q, kv_cache)`` running ``wrapper.run`` with the wrapper's
-    current plan; defines the operator on first use of the name.  Returns the op."""
+    current plan; defines the operator on first use of the name.  Returns the op.  Also
+    defines ``torch.ops.bsx.<name>_with_append(q, k, v, kv_cache)``: the layer's KV update
+    (k / v at the tail of each request, as update_kv with kv_append_indptr = qo_indptr)
+    and its attention in one call, mutating ``kv_cache``."""
     if not name.isidentifier():
         raise ValueError(f"operator name {name!r} must be an identifier")
     if name not in _DEFINED:
-        _DEFINED[name] = _attention_op(name)
+        _DEFINED[name] = (_attention_op(name), _attention_append_op(name))
     _WRAPPERS[name] = wrapper
     return getattr(torch.ops.bsx, name)
 

@@ -27,9 +27,11 @@ Printed: one JSON line with
               limit)
   accepted_tok_s  accepted tokens/s of a 32-layer verify step captured in one graph
               and replayed (verify_step_graph): the page-table insert, one device plan,
-              32 x (append + attention, a KV cache per layer), the fused greedy
+              32 x (append + attention, one launch, a KV cache per layer), the greedy
               acceptance over [64, 5, 128256] bf16 logits (draft = target argmax with
-              probability 0.7, reference rule) and the delete of rejected tokens;
+              probability 0.7, reference rule) fused with the delete of rejected tokens;
+              accepted_tok_s_reference_calls the same step with the reference's calls
+              (append, attention, evaluate_posterior, delete_kv as separate launches);
               accepted_tok_s_sampling the same step with the reference's default
               sampling acceptance instead (sampling_accept_mtp: T=0.6, top_k=20,
               top_p=0.95, one-hot drafts, accept = emitted + 1)
@@ -414,12 +416,13 @@ def verify_step_graph(dev, iters):
     of config 2), captured in one graph and replayed: DevicePageTable.insert_kv of the 5
     draft tokens, one device plan, 32 layers of (paged append + verify attention), each
     layer with its own KV cache, then the acceptance over [64, 5, 128256] bf16 logits
-    and delete_kv of the rejected tokens.  Three graphs: greedy acceptance (draft = target
-    argmax with probability 0.7, reference rule) fused with the delete
-    (evaluate_posterior_and_delete), the same as two calls (evaluate_posterior, then
-    delete_kv), and the reference's default sampling acceptance (T=0.6, top_k=20,
-    top_p=0.95, one-hot drafts).  Returns per graph the replay's GPU time and the tokens
-    it accepted."""
+    and delete_kv of the rejected tokens.  Four graphs: the library's fused calls
+    (append fused into each layer's attention launch, greedy acceptance fused with the
+    delete; draft = target argmax with probability 0.7, reference rule); the reference's
+    per-layer calls (append, then attention) with the fused acceptance + delete; the
+    reference's calls throughout (evaluate_posterior, then delete_kv); and the reference's
+    default sampling acceptance (T=0.6, top_k=20, top_p=0.95, one-hot drafts).  Returns
+    per graph the replay's GPU time and the tokens it accepted."""
     import numpy as np
     import torch
     import batchspec_amd as bsx
@@ -461,10 +464,14 @@ def verify_step_graph(dev, iters):
                HQ, HKV, D, PS, causal=True, q_data_type=torch.bfloat16, on_device=True,
                max_qo_len=S)
         for layer in range(NUM_LAYERS):
+            if mode == "greedy_fused_append":
+                w.run(qs[layer], caches[layer], out=outs[layer], append_key=ks[layer],
+                      append_value=vs[layer])
+                continue
             bsx.append_kv(ks[layer], vs[layer], qo_indptr, caches[layer], pt.paged_kv_indptr,
                           pt.paged_kv_indices, pt.paged_kv_last_page_len)
             w.run(qs[layer], caches[layer], out=outs[layer])
-        if mode == "greedy":
+        if mode in ("greedy", "greedy_fused_append"):
             # the acceptance and the delete it feeds in one argmax + one kernel
             _, acc, _ = bsx.evaluate_posterior_and_delete(gd, gl, pt, S, eos_token_id=-1)
             accept_buf.copy_(acc)
@@ -483,7 +490,7 @@ def verify_step_graph(dev, iters):
              pt.paged_kv_indptr, pt.paged_kv_indices]
     snapshot = [x.clone() for x in state]
     res = {}
-    for mode in ("greedy", "greedy_unfused", "sampling"):
+    for mode in ("greedy_fused_append", "greedy", "greedy_unfused", "sampling"):
         for x, y in zip(state, snapshot):
             x.copy_(y)
         side = torch.cuda.Stream()
@@ -767,6 +774,10 @@ def main() -> int:
                                                  sets[i % 3].qo_indptr, sets[i % 3].cache,
                                                  sets[i % 3].kv_indptr, sets[i % 3].kv_indices,
                                                  sets[i % 3].kv_last_page_len), args.steps, 3)
+    # the same step as one call: the append fused into the attention launch
+    fused_us = time_events(lambda i: wrappers[i % 3].run(
+        sets[i % 3].q, sets[i % 3].cache, out=outs[i % 3], append_key=sets[i % 3].k_new,
+        append_value=sets[i % 3].v_new), args.steps, 3)
     t_attn, t_app = mean(attn_us), mean(app_us)
     a_bytes = mean(abytes)
     achieved = a_bytes / (t_attn * 1e-6) / 1e9
@@ -795,6 +806,7 @@ def main() -> int:
         "attn_us": round(t_attn, 2),
         "attn_us_median": round(median(attn_us), 2),
         "append_us": round(t_app, 2),
+        "append_attention_fused_us": round(mean(fused_us), 2),
         "append_GBs": round(mean(pbytes) / t_app / 1e3, 1),
         "attn_bytes": int(a_bytes),
         "plan": {"workgroups": int(p0.num_ctas), "segments": int(p0.num_segments),
@@ -834,10 +846,11 @@ def main() -> int:
             n_samp = int(acc_samp.sum())
             # accepted tokens per second of the replayed step (the logits and drafts are
             # the acceptance's own, so each replay accepts the same tokens)
-            result["accepted_tok_s"] = vs["greedy"]["accepted_tok_s"]
+            result["accepted_tok_s"] = vs["greedy_fused_append"]["accepted_tok_s"]
+            result["accepted_tok_s_reference_calls"] = vs["greedy_unfused"]["accepted_tok_s"]
             result["accepted_tok_s_sampling"] = vs["sampling"]["accepted_tok_s"]
             result["accepted_tok_s_prefix_rule"] = round(
-                n_pre / (vs["greedy"]["us"] * 1e-6), 1)
+                n_pre / (vs["greedy_fused_append"]["us"] * 1e-6), 1)
             result["mean_accept_len"] = {"reference_rule": n_ref / 64, "prefix_rule": n_pre / 64,
                                          "sampling": n_samp / 64}
             # the same step as a sum of the separately timed parts, attention on the device

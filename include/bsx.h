@@ -196,6 +196,25 @@ int bsx_attn_run(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d,
                  const int32_t* kv_indices_d, const uint32_t* mask_words_d,
                  void* out_d, int64_t out_stride_tok, float* lse_d, void* stream);
 
+/* The layer's KV update and its attention in one call: StandardKVCache.update(k, v,
+ * kv_append_indptr = qo_indptr, page_table) (batchspec/models/modules/kv_cache.py:47-84,
+ * called at batchspec/models/modules/attention/standard.py:63-66) followed by run(q,
+ * kv_cache) (standard.py:69).  Arguments of bsx_attn_run, plus the appended rows
+ * k_new_d / v_new_d [total_qo, num_kv_heads, head_dim] (token strides in elements):
+ * token i of request b goes to position kv_len_b - qo_len_b + i of the cache, where the
+ * plan's page table already counts it.  With pages of at least 16 tokens and the per-wave
+ * kernel the append is fused into the attention launch (the appended rows are read from
+ * k_new_d / v_new_d and written to the cache by the workgroup that attends to the
+ * request's last tile); otherwise one append launch precedes the attention.  Outputs
+ * and cache contents equal bsx_kv_append followed by bsx_attn_run. */
+int bsx_attn_run_append(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d,
+                        void* float_ws_d, int dtype, const void* q_d, int64_t q_stride_tok,
+                        const void* k_cache_d, const void* v_cache_d, int64_t page_stride,
+                        const int32_t* kv_indices_d, const uint32_t* mask_words_d,
+                        void* out_d, int64_t out_stride_tok, float* lse_d,
+                        const void* k_new_d, int64_t k_new_stride_tok, const void* v_new_d,
+                        int64_t v_new_stride_tok, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* 2. Paged KV append                                                         */
 /* ------------------------------------------------------------------------- */

@@ -55,6 +55,18 @@ def test_layer_of_update_kv_and_attention_is_one_graph():
     assert "torch.ops.bsx.update_kv" in code and "torch.ops.bsx.attn_draft_and_verify" in code
 
 
+def test_fused_update_and_attention_operator_traces():
+    ops.bind_attention("attn_verify_fused", _Unrun())
+    graphs = []
+    f = torch.compile(lambda q, k, v, c: torch.ops.bsx.attn_verify_fused_with_append(q, k, v, c),
+                      backend=_fake_backend(graphs), fullgraph=True)
+    q = torch.zeros(10, 32, 128, dtype=torch.bfloat16)
+    k = torch.zeros(10, 8, 128, dtype=torch.bfloat16)
+    cache = torch.zeros(4, 2, 16, 8, 128, dtype=torch.bfloat16)
+    out = f(q, k, k, cache)
+    assert out.shape == q.shape and len(graphs) == 1
+
+
 def test_acceptance_operators_trace_with_the_reference_dtypes():
     graphs = []
     be = _fake_backend(graphs)
