@@ -466,8 +466,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
         qo_indptr, batchspec/models/modules/kv_cache.py:47-84, as
         batchspec/models/modules/attention/standard.py:63-66 calls it) and attention sees
         them, as the update followed by run() does.  The plan's page table must already
-        count those tokens (insert_kv runs before the layers).  Fused into the attention
-        launch for the per-wave kernel with pages of at least 16 tokens."""
+        count those tokens (insert_kv runs before the layers).  One launch: the
+        attention kernel writes the rows into the cache before reading them."""
         plan = self._plan
         if plan is None:
             raise RuntimeError("plan() must be called before run()")

@@ -389,16 +389,48 @@ __device__ __forceinline__ void row_masks(const Params& p, const Seg& cur, int r
   }
 }
 
-// NT: query-row tiles of 16 per wave.  D: head dim (64 or 128).  APPEND (pages of at
-// least 16 tokens): the rows in p.k_new / p.v_new are this step's draft tokens, not yet in
-// the cache.  Their K/V loads read those rows instead of the cache (a per-lane address
-// select, only in the subtiles that hold them), and the workgroup that attends to a
-// request's last tile writes them into their page slots for later steps; nothing in this
-// launch reads those slots, so no ordering is needed.  The result equals the separate
-// append followed by attention bit for bit, with one launch less per layer.
-template <int DT, int D, int NT, bool PS_GE16, bool APPEND = false>
+// The layer's KV update fused into the attention launch (p.k_new != null).  Every
+// workgroup whose segments reach a request's appended rows (tiles past kv_len - qo_len)
+// first writes those rows, for its own kv heads, from p.k_new / p.v_new into their page
+// slots and meets its waves at a barrier, which waits for the stores; its tile loads after
+// that read the rows from the cache like any other.  Workgroups that share a request write
+// the same bytes into the same slots, and none reads an appended slot without having
+// written it first, so no read sees a slot's old contents.  The result equals the append
+// followed by the attention launch bit for bit.  Rows at negative positions (kv_len below
+// qo_len) have no slot and are skipped, as the standalone append skips them.
+template <int D>
+__device__ void append_rows_of_segments(const Params& p, int seg_begin, int seg_end, int hgroup) {
+  constexpr int PIECES = D * 2 / 16;  // 16-byte pieces of a row's head slice
+  const int64_t tok_bytes = (int64_t)p.num_kv_heads * D * 2;
+  const int per_row = p.heads_per_cta * PIECES;
+  const int64_t col0 = (int64_t)hgroup * p.heads_per_cta * D * 2;
+  for (int si = seg_begin; si < seg_end; ++si) {
+    const Seg s = load_seg(p, si);
+    const int diag = s.kv_len - s.qo_len;
+    if (s.t0 >= s.t1 || s.t1 * kTile <= diag) continue;  // reads no appended row
+    for (int idx = threadIdx.x; idx < s.qo_len * per_row; idx += blockDim.x) {
+      const int i = idx / per_row;
+      const int pos = diag + i;
+      if (pos < 0) continue;
+      const int64_t col = col0 + (int64_t)(idx - i * per_row) * 16;
+      const int page = p.kv_indices[s.page_start + (pos >> p.page_shift)];
+      const int64_t dst =
+          (int64_t)page * p.page_stride_bytes + (int64_t)(pos & p.page_mask) * tok_bytes + col;
+      const int64_t src = s.qo_start + i;
+      const u32x4 kv = *reinterpret_cast<const u32x4*>(
+          reinterpret_cast<const char*>(p.k_new + src * p.knew_stride) + col);
+      const u32x4 vv = *reinterpret_cast<const u32x4*>(
+          reinterpret_cast<const char*>(p.v_new + src * p.vnew_stride) + col);
+      *reinterpret_cast<u32x4*>(const_cast<char*>(p.k_cache) + dst) = kv;
+      *reinterpret_cast<u32x4*>(const_cast<char*>(p.v_cache) + dst) = vv;
+    }
+  }
+  __syncthreads();
+}
+
+// NT: query-row tiles of 16 per wave.  D: head dim (64 or 128).
+template <int DT, int D, int NT, bool PS_GE16>
 __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
-  static_assert(!APPEND || PS_GE16, "the fused append needs pages of at least 16 tokens");
   constexpr int KS = D / 32;  // k-steps of the QK^T contraction
   constexpr int NJ = D / 16;  // output d tiles (also d values per lane in V loads)
   constexpr int QT = 16 * NT;
@@ -425,6 +457,7 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
   const int seg_begin = ld_uniform(p.blob, p.off_seg_indptr + blockIdx.x);
   const int seg_end = ld_uniform(p.blob, p.off_seg_indptr + blockIdx.x + 1);
   if (seg_begin >= seg_end) return;
+  if (p.k_new != nullptr) append_rows_of_segments<D>(p, seg_begin, seg_end, hgroup);
 
   const int g = p.group;
   const int64_t tok_bytes = (int64_t)p.num_kv_heads * D * 2;  // one kv token row (all heads)
@@ -441,9 +474,7 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
   auto page_pos = [&](int jsc, int kv_len, int page_start) -> int {
     return kv_len > 0 ? page_start + (jsc >> p.page_shift) : p.safe_pos;
   };
-  // (qo_start, diag = kv_len - qo_len: where the request's appended rows start; used
-  // with APPEND only)
-  auto load_tile_k = [&](int tile, int kv_len, int page_start, int qo_start, int diag) {
+  auto load_tile_k = [&](int tile, int kv_len, int page_start) {
     const int j0 = tile * kTile;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -461,20 +492,11 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
         base = p.k_cache + (int64_t)page * p.page_stride_bytes;
         off = (uint32_t)((j & p.page_mask) * tok_bytes) + head_off;
       }
-      const char* addr = base + off;
-      if constexpr (APPEND) {
-        if (js + 16 > diag) {  // uniform: the subtile holds appended rows
-          const int j = js + c16;
-          const char* na = reinterpret_cast<const char*>(
-              p.k_new + (int64_t)(qo_start + j - diag) * p.knew_stride) + head_off;
-          addr = (j >= diag && j < kv_len) ? na : addr;
-        }
-      }
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kreg[st][s] = ld_stream(addr + (32 * s + 8 * g4) * 2);
+      for (int s = 0; s < KS; ++s) kreg[st][s] = ld_stream(base + off + (32 * s + 8 * g4) * 2);
     }
   };
-  auto load_tile_v = [&](int tile, int kv_len, int page_start, int qo_start, int diag) {
+  auto load_tile_v = [&](int tile, int kv_len, int page_start) {
     const int j0 = tile * kTile;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -487,7 +509,6 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
         sbase = p.v_cache + (int64_t)page * p.page_stride_bytes;
         soff = (uint32_t)((jsc & p.page_mask) * tok_bytes) + head_off;
       }
-      const bool sub_new = APPEND && js + 16 > diag;  // uniform
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         const int e = 4 * st + e4;
@@ -503,24 +524,14 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
           off = (uint32_t)((j & p.page_mask) * tok_bytes) + head_off;
         }
         off += (uint32_t)(NJ * c16 * 2);
-        const char* addr = base + off;
-        if constexpr (APPEND) {
-          if (sub_new) {
-            const int j = js + 4 * g4 + e4;
-            const char* na = reinterpret_cast<const char*>(
-                p.v_new + (int64_t)(qo_start + j - diag) * p.vnew_stride) + head_off +
-                NJ * c16 * 2;
-            addr = (j >= diag && j < kv_len) ? na : addr;
-          }
-        }
         if constexpr (VW == 4) {
-          const u32x4 v = ld_stream(addr);
+          const u32x4 v = ld_stream(base + off);
           vraw[e][0] = v[0];
           vraw[e][1] = v[1];
           vraw[e][2] = v[2];
           vraw[e][3] = v[3];
         } else {
-          const u32x2 v = ld_stream2(addr);
+          const u32x2 v = ld_stream2(base + off);
           vraw[e][0] = v[0];
           vraw[e][1] = v[1];
         }
@@ -530,8 +541,8 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
 
   Seg cur = load_seg(p, seg_begin);
   Seg nxt = load_seg(p, min(seg_begin + 1, seg_end - 1));
-  load_tile_k(cur.t0, cur.kv_len, cur.page_start, cur.qo_start, cur.kv_len - cur.qo_len);
-  load_tile_v(cur.t0, cur.kv_len, cur.page_start, cur.qo_start, cur.kv_len - cur.qo_len);
+  load_tile_k(cur.t0, cur.kv_len, cur.page_start);
+  load_tile_v(cur.t0, cur.kv_len, cur.page_start);
 
   for (int si = seg_begin; si < seg_end; ++si) {
     const bool has_next = si + 1 < seg_end;
@@ -579,8 +590,6 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
     const int end_tile = has_next ? nxt.t0 : max(cur.t1 - 1, 0);
     const int end_kv = has_next ? nxt.kv_len : cur.kv_len;
     const int end_pages = has_next ? nxt.page_start : cur.page_start;
-    const int end_qo = has_next ? nxt.qo_start : cur.qo_start;
-    const int end_diag = has_next ? nxt.kv_len - nxt.qo_len : diag;
 
     // One tile: S^T = K Q^T, softmax, O^T += V^T P^T, with the next tile's K and V
     // loads issued as soon as their registers are free.  MASKED is a compile-time
@@ -594,8 +603,6 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       const int pf_tile = last ? end_tile : tile + 1;
       const int pf_kv = last ? end_kv : cur.kv_len;
       const int pf_pages = last ? end_pages : cur.page_start;
-      const int pf_qo = last ? end_qo : cur.qo_start;
-      const int pf_diag = last ? end_diag : diag;
       // Workgroup barrier without a memory fence (the tile loads in flight stay in
       // flight).  The asm also keeps the Q reads from LDS inside the loop instead of
       // letting them be hoisted into registers the pipelined tiles need.
@@ -618,7 +625,7 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       // place (a load hoisted above those reads would need fresh registers and a copy
       // at the loop back-edge that waits for the load to complete).
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (PREFETCH) load_tile_k(pf_tile, pf_kv, pf_pages, pf_qo, pf_diag);
+      if constexpr (PREFETCH) load_tile_k(pf_tile, pf_kv, pf_pages);
 
       if constexpr (MASKED) mask_tile<NT>(sacc, rm, j0, g4, diag, sink_end, win_beg);
 
@@ -634,7 +641,7 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
 #pragma unroll
       for (int jm = 0; jm < NJ; ++jm) asm volatile("" ::"v"(va[jm]) : "memory");
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (PREFETCH) load_tile_v(pf_tile, pf_kv, pf_pages, pf_qo, pf_diag);  // V registers are free
+      if constexpr (PREFETCH) load_tile_v(pf_tile, pf_kv, pf_pages);  // V registers are free
       pv_tile<DT, NJ, NT>(va, pb, o);
     };
 
@@ -655,36 +662,11 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
     } else if (has_next) {
       // No tile ran, so the prefetched tile was not consumed: load the next
       // segment's first tile now.
-      load_tile_k(end_tile, end_kv, end_pages, end_qo, end_diag);
-      load_tile_v(end_tile, end_kv, end_pages, end_qo, end_diag);
+      load_tile_k(end_tile, end_kv, end_pages);
+      load_tile_v(end_tile, end_kv, end_pages);
     }
 
     finish_segment<DT, D, NT>(p, cur, h, row0, c16, g4, o, m_ref, l_run);
-
-    if constexpr (APPEND) {
-      // this segment holds the request's last tile: its workgroup writes the appended
-      // rows into their page slots (one wave per kv head, 16-byte pieces of the head's
-      // slice of each row; nothing in this launch reads those slots)
-      if (has_tiles && cur.t1 * kTile >= cur.kv_len && qb == 0) {
-        constexpr int PER_ROW = D * 2 / 16;  // 16-byte pieces of a row's head slice
-        for (int i = lane / PER_ROW; i < cur.qo_len; i += 64 / PER_ROW) {
-          const int pos = diag + i;
-          const int page = p.kv_indices[cur.page_start + (pos >> p.page_shift)];
-          const int64_t dst = (int64_t)page * p.page_stride_bytes +
-                              (int64_t)(pos & p.page_mask) * tok_bytes + head_off +
-                              (lane % PER_ROW) * 16;
-          const int64_t src = (int64_t)(cur.qo_start + i);
-          const u32x4 kv = *reinterpret_cast<const u32x4*>(
-              reinterpret_cast<const char*>(p.k_new + src * p.knew_stride) + head_off +
-              (lane % PER_ROW) * 16);
-          const u32x4 vv = *reinterpret_cast<const u32x4*>(
-              reinterpret_cast<const char*>(p.v_new + src * p.vnew_stride) + head_off +
-              (lane % PER_ROW) * 16);
-          *reinterpret_cast<u32x4*>(const_cast<char*>(p.k_cache) + dst) = kv;
-          *reinterpret_cast<u32x4*>(const_cast<char*>(p.v_cache) + dst) = vv;
-        }
-      }
-    }
 
     cur = nxt;
     nxt = load_seg(p, min(si + 2, seg_end - 1));
@@ -768,6 +750,7 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
   const int seg_begin = ld_uniform(p.blob, p.off_seg_indptr + blockIdx.x);
   const int seg_end = ld_uniform(p.blob, p.off_seg_indptr + blockIdx.x + 1);
   if (seg_begin >= seg_end) return;
+  if (p.k_new != nullptr) append_rows_of_segments<D>(p, seg_begin, seg_end, hgroup);
 
   const int g = p.group;
   const uint32_t tok_bytes = (uint32_t)(p.num_kv_heads * D * 2);
@@ -1107,37 +1090,12 @@ __global__ void __launch_bounds__(256) empty_kernel(Params p, int total_qo) {
   if (p.lse_out != nullptr && c < p.num_qo_heads) p.lse_out[t * p.num_qo_heads + c] = -INFINITY;
 }
 
-template <int DT, int D, int NT, bool PS16, bool APPEND = false>
+template <int DT, int D, int NT, bool PS16>
 static int launch_main(const bsx_attn_plan_t* plan, const Params& prm, int waves, hipStream_t st) {
   dim3 grid(plan->num_ctas, (plan->num_kv_heads / plan->heads_per_cta) * prm.n_qgroups);
-  hipLaunchKernelGGL((verify_attn_kernel<DT, D, NT, PS16, APPEND>), grid, dim3(64 * waves), 0, st,
-                     prm);
+  hipLaunchKernelGGL((verify_attn_kernel<DT, D, NT, PS16>), grid, dim3(64 * waves), 0, st, prm);
   BSX_LAUNCH_CHECK();
   return BSX_OK;
-}
-
-// The append of p.k_new / p.v_new on its own, for the kernels that do not fuse it (shared
-// K/V tiles, pages below 16 tokens): one workgroup per request, from the plan's request
-// records (token i of request b to position kv_len_b - qo_len_b + i), 16-byte pieces.
-__global__ void __launch_bounds__(256) append_from_plan_kernel(Params p, int64_t tok_bytes) {
-  const int32_t* sq = p.blob + p.off_seq + 4 * blockIdx.x;
-  const int qo_start = sq[0], qo_len = sq[1], kv_len = sq[2], page_start = sq[3];
-  const int diag = kv_len - qo_len;
-  const int pieces = (int)(tok_bytes / 16);
-  for (int idx = threadIdx.x; idx < qo_len * pieces; idx += blockDim.x) {
-    const int i = idx / pieces;
-    const int c = idx - i * pieces;
-    const int pos = diag + i;
-    const int page = p.kv_indices[page_start + (pos >> p.page_shift)];
-    const int64_t dst = (int64_t)page * p.page_stride_bytes + (int64_t)(pos & p.page_mask) * tok_bytes +
-                        (int64_t)c * 16;
-    const u32x4 kv = *reinterpret_cast<const u32x4*>(
-        reinterpret_cast<const char*>(p.k_new + (int64_t)(qo_start + i) * p.knew_stride) + c * 16);
-    const u32x4 vv = *reinterpret_cast<const u32x4*>(
-        reinterpret_cast<const char*>(p.v_new + (int64_t)(qo_start + i) * p.vnew_stride) + c * 16);
-    *reinterpret_cast<u32x4*>(const_cast<char*>(p.k_cache) + dst) = kv;
-    *reinterpret_cast<u32x4*>(const_cast<char*>(p.v_cache) + dst) = vv;
-  }
 }
 
 template <int DT, int D, int QB>
@@ -1161,27 +1119,17 @@ static int launch_all(const bsx_attn_plan_t* plan, const Params& prm, hipStream_
   }
   const int waves = plan->heads_per_cta * prm.qblocks_per_cta;
   const bool ps16 = plan->page_size >= 16;
-  const bool append = prm.k_new != nullptr;
-  const bool fused = append && ps16 && !plan->shared_kv_tiles;
-  if (append && !fused) {
-    // the append first, then attention reading the cache
-    hipLaunchKernelGGL(append_from_plan_kernel, dim3((unsigned)plan->batch), dim3(256), 0, st,
-                       prm, (int64_t)plan->num_kv_heads * D * 2);
-    BSX_LAUNCH_CHECK();
-  }
   int rc;
   if (plan->shared_kv_tiles) {
     rc = plan->qblocks_per_cta == 2   ? launch_shared<DT, D, 2>(plan, prm, st)
          : plan->qblocks_per_cta == 4 ? launch_shared<DT, D, 4>(plan, prm, st)
                                       : launch_shared<DT, D, 8>(plan, prm, st);
   } else if (plan->qrow_tile == 16) {
-    rc = fused  ? launch_main<DT, D, 1, true, true>(plan, prm, waves, st)
-         : ps16 ? launch_main<DT, D, 1, true>(plan, prm, waves, st)
-                : launch_main<DT, D, 1, false>(plan, prm, waves, st);
+    rc = ps16 ? launch_main<DT, D, 1, true>(plan, prm, waves, st)
+              : launch_main<DT, D, 1, false>(plan, prm, waves, st);
   } else {
-    rc = fused  ? launch_main<DT, D, 2, true, true>(plan, prm, waves, st)
-         : ps16 ? launch_main<DT, D, 2, true>(plan, prm, waves, st)
-                : launch_main<DT, D, 2, false>(plan, prm, waves, st);
+    rc = ps16 ? launch_main<DT, D, 2, true>(plan, prm, waves, st)
+              : launch_main<DT, D, 2, false>(plan, prm, waves, st);
   }
   if (rc != BSX_OK || plan->num_split_requests == 0) return rc;
   constexpr int RPB = 256 / (D / 8);

@@ -202,11 +202,10 @@ int bsx_attn_run(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d,
  * kv_cache) (standard.py:69).  Arguments of bsx_attn_run, plus the appended rows
  * k_new_d / v_new_d [total_qo, num_kv_heads, head_dim] (token strides in elements):
  * token i of request b goes to position kv_len_b - qo_len_b + i of the cache, where the
- * plan's page table already counts it.  With pages of at least 16 tokens and the per-wave
- * kernel the append is fused into the attention launch (the appended rows are read from
- * k_new_d / v_new_d and written to the cache by the workgroup that attends to the
- * request's last tile); otherwise one append launch precedes the attention.  Outputs
- * and cache contents equal bsx_kv_append followed by bsx_attn_run. */
+ * plan's page table already counts it.  One launch: each workgroup whose tiles reach a
+ * request's appended rows first writes them (for its kv heads) into the cache, then reads
+ * them back with the other rows.  Outputs and cache contents equal bsx_kv_append followed
+ * by bsx_attn_run; rows at negative positions (kv_len < qo_len) are skipped, as there. */
 int bsx_attn_run_append(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d,
                         void* float_ws_d, int dtype, const void* q_d, int64_t q_stride_tok,
                         const void* k_cache_d, const void* v_cache_d, int64_t page_stride,

@@ -3,10 +3,12 @@ bsx_attn_run_append) against the two calls it replaces: StandardKVCache.update w
 kv_append_indptr = qo_indptr (batchspec/models/modules/kv_cache.py:47-84, called at
 batchspec/models/modules/attention/standard.py:63-66) and then run() (standard.py:69).
 Outputs, lse and the whole cache must be equal bit for bit, over host and device plans,
-the per-wave kernel with one and two row tiles (the fused path), the shared-tile kernel and
-pages below 16 tokens (a separate append launch inside the call), ragged batches whose
-appended rows cross tile and page boundaries, split requests, causal / tree / sink+window
-masks and both 16-bit types; and the eager result is checked against the fp32 oracle."""
+the per-wave kernel with one and two row tiles, the shared-tile kernel, pages below 16
+tokens, several query groups per kv head (workgroups writing the same rows), ragged
+batches whose appended rows cross tile and page boundaries, split requests, causal / tree /
+sink+window masks and both 16-bit types; and the eager result is checked against the fp32
+oracle.  The starting cache holds random rows in the appended slots, so a read of a slot
+before its write would show."""
 import sys
 
 import numpy as np
@@ -92,8 +94,9 @@ def test_ragged_appends_across_tiles_pages_and_splits(hq, hkv, dtype):
     AP.check(got[0], ref[0], got[1], ref[1])
 
 
-def test_tree_and_small_pages_take_the_separate_append():
-    say("fused-call API on the shared-tile kernel (trees) and on 8-token pages")
+def test_tree_small_pages_and_query_groups():
+    say("fused append on the shared-tile kernel (trees), on 8-token pages, and with several "
+        "query groups per kv head")
     t = make_verify_batch(6, 100, 3000, 32, 32, 8, 128, 16, dtype=torch.bfloat16, seed=8,
                           tree_nodes=32, device=DEV)
     wt = _wrapper(t, causal=False, tree_mask_words=t.mask_words)
@@ -104,6 +107,15 @@ def test_tree_and_small_pages_take_the_separate_append():
     ws = _wrapper(s, causal=True)
     got, want = _both(s, ws)
     _equal(got, want, "page size 8")
+    for ps in (16, 8):  # 80 drafts x group 4 = 320 rows: two query groups per kv head
+        d = make_verify_batch(4, 200, 3000, 80, 32, 8, 128, ps, dtype=torch.bfloat16,
+                              seed=11 + ps, device=DEV)
+        wd = _wrapper(d, causal=True)
+        assert wd.plan_info.num_qgroups > 1
+        got, want = _both(d, wd)
+        _equal(got, want, f"two query groups, page size {ps}")
+        ref = AP.oracle_per_request(_with_cache(d, want[2]), "causal")[None]
+        AP.check(got[0], ref[0], got[1], ref[1])
 
 
 def test_streaming_view_with_append():
