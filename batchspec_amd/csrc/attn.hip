@@ -190,13 +190,11 @@ __device__ __forceinline__ void mask_tile(f32x4 (&sacc)[2][NT], const RowMask (&
 // scaled by scale_log2).  The reference is raised, and O and l rescaled, only when some
 // row's scaled maximum exceeds it by more than the margin (always on the first visible
 // tile).  Returns the probabilities packed as the B operand of O^T += V^T P^T.  The row
-// sums go to l_run (this lane's share) or, with MMA_L, are left to the caller's matrix
-// accumulator lacc (rescaled here with O).
-template <int DT, int NJ, int NT, bool MMA_L = false>
+// sums go to l_run (this lane's share).
+template <int DT, int NJ, int NT>
 __device__ __forceinline__ void softmax_tile(const f32x4 (&sacc)[2][NT], float scale_log2,
                                              float (&m_ref)[NT], float (&l_run)[NT],
-                                             f32x4 (&o)[NJ][NT], uint32_t (&pb)[NT][4],
-                                             f32x4* lacc = nullptr) {
+                                             f32x4 (&o)[NJ][NT], uint32_t (&pb)[NT][4]) {
   bool need = false;
   float tmax[NT];
 #pragma unroll
@@ -216,10 +214,7 @@ __device__ __forceinline__ void softmax_tile(const f32x4 (&sacc)[2][NT], float s
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_ref[nt], mx);
       const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref[nt] - m_new);
-      if constexpr (MMA_L)
-        lacc[nt] *= alpha;
-      else
-        l_run[nt] *= alpha;
+      l_run[nt] *= alpha;
 #pragma unroll
       for (int jm = 0; jm < NJ; ++jm) o[jm][nt] *= alpha;
       m_ref[nt] = m_new;
@@ -232,7 +227,7 @@ __device__ __forceinline__ void softmax_tile(const f32x4 (&sacc)[2][NT], float s
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[e >> 2][nt][e & 3], scale_log2, neg_m));
-      if constexpr (!MMA_L) l_run[nt] += pv[e];
+      l_run[nt] += pv[e];
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) pb[nt][r] = pack2<DT>(pv[2 * r], pv[2 * r + 1]);
@@ -310,9 +305,8 @@ __device__ __forceinline__ void store_row(uint16_t* dst, int g4, const f32x4 (&o
   }
 }
 
-// l_run: this lane's share of the row sums (summed over the 4 lane groups here), or,
-// with L_COMPLETE, the whole row sums.
-template <int DT, int D, int NT, bool INTERLEAVED = true, bool L_COMPLETE = false>
+// l_run: this lane's share of the row sums (summed over the 4 lane groups here).
+template <int DT, int D, int NT, bool INTERLEAVED = true>
 __device__ __forceinline__ void finish_segment(const Params& p, const Seg& cur, int h, int row0,
                                                int c16, int g4, f32x4 (&o)[D / 16][NT],
                                                const float (&m_ref)[NT],
@@ -325,10 +319,8 @@ __device__ __forceinline__ void finish_segment(const Params& p, const Seg& cur, 
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     float l = l_run[nt];
-    if constexpr (!L_COMPLETE) {
-      l += __shfl_xor(l, 16);
-      l += __shfl_xor(l, 32);
-    }
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
     const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
     for (int jm = 0; jm < NJ; ++jm) o[jm][nt] *= inv;
@@ -911,18 +903,12 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
     for (int jm = 0; jm < NJ; ++jm)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) o[jm][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_ref[NT], l_run[NT];
-    // Row sums on the matrix core: lacc[nt] += ONES P^T, every element of lane
-    // (c16, g4) is the sum for row c16 (of the same 16-bit P the output uses).
-    f32x4 lacc[NT];
+    float m_ref[NT], l_run[NT];  // l_run: this lane's share of the row sum
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       m_ref[nt] = -INFINITY;
       l_run[nt] = 0.f;
-      lacc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    constexpr uint32_t kOne2 = DT == BSX_DTYPE_BF16 ? 0x3F803F80u : 0x3C003C00u;
-    const u32x4 ones = {kOne2, kOne2, kOne2, kOne2};
 
     auto tile_step = [&](int tile, auto masked_tag) {
       constexpr bool MASKED = decltype(masked_tag)::value;
@@ -968,7 +954,7 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
       }
       if constexpr (MASKED) mask_tile<NT>(sacc, rm, j0, g4, diag, sink_end, win_beg);
       uint32_t pb[NT][4];
-      softmax_tile<DT, NJ, NT, true>(sacc, p.scale_log2, m_ref, l_run, o, pb, lacc);
+      softmax_tile<DT, NJ, NT>(sacc, p.scale_log2, m_ref, l_run, o, pb);
       if constexpr (MASKED) {
         // V rows of tokens at or past kv_len hold unrelated data: zero them (element
         // e of va[jm] is token tau(g4, e))
@@ -984,11 +970,6 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
           for (int r = 0; r < 4; ++r) va[jm][r] &= keep[r];
       }
       pv_tile<DT, NJ, NT>(va, pb, o);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        u32x4 bop = {pb[nt][0], pb[nt][1], pb[nt][2], pb[nt][3]};
-        lacc[nt] = mfma16x16x32<DT>(ones, bop, lacc[nt]);
-      }
       ++n;
     };
 
@@ -999,9 +980,7 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
       for (int tile = cur.t0; tile < t_split; ++tile) tile_step(tile, std::false_type());
       for (int tile = t_split; tile < cur.t1; ++tile) tile_step(tile, std::true_type());
     }
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) l_run[nt] = lacc[nt][0];
-    finish_segment<DT, D, NT, false, true>(p, cur, h, row0, c16, g4, o, m_ref, l_run);
+    finish_segment<DT, D, NT, false>(p, cur, h, row0, c16, g4, o, m_ref, l_run);
   }
   // No direct load may still target this workgroup's LDS when it exits.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
