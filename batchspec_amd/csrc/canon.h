@@ -6,10 +6,11 @@
 //   * exp is our own: 2^y = ldexp(P(f), n), n = floor(y) saturated to the int32 range,
 //     f = fl(y - n) capped at the largest float below 1 (the GPU's v_cvt_flr_i32_f32
 //     and v_fract_f32, the latter with its clamp modifier, so that f = 0 for an
-//     infinite y), P a degree-5 polynomial with P(0) = 1 fitted to 2^f on [0, 1) for
-//     relative error (Lawson iteration, coefficients rounded to binary32 and tuned in
-//     the last bit), evaluated by Horner with fused multiply-add; at most 3 ulp from
-//     2^y.  exp2(-inf) = 0 (n = INT_MIN); arguments far below -150 underflow to 0 in
+//     infinite y), P a degree-4 polynomial with P(0) = 1 fitted to 2^f on [0, 1) for
+//     relative error (minimax by linear programming over 20000 points of [0, 1),
+//     coefficients rounded to binary32; no last-bit change of them does better),
+//     evaluated by Horner with fused multiply-add; relative error at most 3.0e-6 from
+//     2^y (P(f) < 2 at the largest f, and P rises with f).  exp2(-inf) = 0 (n = INT_MIN); arguments far below -150 underflow to 0 in
 //     ldexp without a clamp.
 //   * every sum runs over a fixed tree, independent of the launch configuration:
 //       - a row of V values is cut into groups of 8 consecutive elements
@@ -56,11 +57,10 @@ constexpr int kLaneStride = kLanes;                  // groups between consecuti
 
 constexpr float kLog2e = 0x1.715476p+0f;
 constexpr float kC0 = 0x1.0p+0f;
-constexpr float kC1 = 0x1.62e4bap-1f;
-constexpr float kC2 = 0x1.ebdb5ap-3f;
-constexpr float kC3 = 0x1.c91ce4p-5f;
-constexpr float kC4 = 0x1.277854p-7f;
-constexpr float kC5 = 0x1.e974f6p-10f;
+constexpr float kC1 = 0x1.62d6c2p-1f;
+constexpr float kC2 = 0x1.ee24b2p-3f;
+constexpr float kC3 = 0x1.abf636p-5f;
+constexpr float kC4 = 0x1.b7fb26p-7f;
 
 // 2^y = ldexp(P(f), n): returns P(f) and sets n.
 BSX_HD float exp2_parts(float y, int* n_out) {
@@ -81,8 +81,7 @@ BSX_HD float exp2_parts(float y, int* n_out) {
     n = fl >= 0x1p31f ? INT32_MAX : (fl < -0x1p31f ? INT32_MIN : (int)fl);
   }
 #endif
-  float p = kC5;
-  p = fmaf(p, f, kC4);
+  float p = kC4;
   p = fmaf(p, f, kC3);
   p = fmaf(p, f, kC2);
   p = fmaf(p, f, kC1);

@@ -1095,9 +1095,16 @@ struct SplitArgs {
 // the lower edge of the first bin, from the top, at which k keys are reached.  At least
 // k of the keys are at or above it, and it is within one bf16 step of the k-th largest.
 // Returns 0 when the k largest do not fit the 256 bins (or there are fewer than k).
-// Every thread calls it; uses hist, part and bin of L.
+// Every thread calls it; uses hist, part and bin of L.  Its barriers order only LDS
+// (s_waitcnt lgkmcnt(0); s_barrier): global loads the caller has in flight stay in
+// flight across it when it is inlined (fine_bound_inline).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int N>
-__device__ __noinline__ uint32_t fine_bound(RowsLds& L, const uint32_t (&key)[N], int k) {
+__device__ __forceinline__ uint32_t fine_bound_inline(RowsLds& L, const uint32_t (&key)[N],
+                                                      int k) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   uint32_t kmax = 0u;
 #pragma unroll
@@ -1106,7 +1113,7 @@ __device__ __noinline__ uint32_t fine_bound(RowsLds& L, const uint32_t (&key)[N]
   for (int m = 1; m < 64; m <<= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, m));
   if (lane == 0) L.part[wave] = kmax;
   L.hist[t] = 0u;
-  __syncthreads();
+  lds_barrier();
   kmax = max(max(L.part[0], L.part[1]), max(L.part[2], L.part[3]));
   const uint32_t top = kmax >> 16;
 #pragma unroll
@@ -1114,7 +1121,7 @@ __device__ __noinline__ uint32_t fine_bound(RowsLds& L, const uint32_t (&key)[N]
     const uint32_t d = top - (key[i] >> 16);
     if (key[i] != 0u && d < 256u) atomicAdd(&L.hist[d], 1u);
   }
-  __syncthreads();
+  lds_barrier();
   if (t < 64) {
     const u32x4 c = reinterpret_cast<const u32x4*>(L.hist)[t];
     const uint32_t s = (c[0] + c[1]) + (c[2] + c[3]);
@@ -1142,10 +1149,15 @@ __device__ __noinline__ uint32_t fine_bound(RowsLds& L, const uint32_t (&key)[N]
     }
     if (t == 0) L.bin = kmax == 0u ? -1 : bin;
   }
-  __syncthreads();
+  lds_barrier();
   const int bin = L.bin;
-  __syncthreads();
+  lds_barrier();
   return bin < 0 ? 0u : (top - (uint32_t)bin) << 16;
+}
+
+template <int N>
+__device__ __noinline__ uint32_t fine_bound(RowsLds& L, const uint32_t (&key)[N], int k) {
+  return fine_bound_inline<N>(L, key, k);
 }
 
 template <int DT>
@@ -1264,12 +1276,30 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
     }
   };
 
+  // The rounds after round 0 that are whole for every thread of the part run in batches
+  // of kSplitRounds, software-pipelined over two register sets: each batch's loads go
+  // out before the previous batch is computed, so a wave's arithmetic overlaps its own
+  // loads (the workgroups of all rows start together and would otherwise alternate
+  // between loading and computing in step).  Rounds [8, c_whole) are whole for every
+  // thread of the part (its largest canonical thread is the binding one), in whole
+  // batches; the rounds after them (at most a few) take do_round's per-group rules.
+  constexpr int NR = kSplitRounds;
+  const std::integral_constant<int, NR> nr;
+  const int64_t ct_max = (int64_t)p * kPartThreads + kPartThreads - 1;
+  const int64_t n_whole = G_whole > ct_max + 256 * 7 ? (G_whole - 1 - ct_max - 256 * 7) / 2048 + 1 : 0;
+  const int64_t c_whole = 8 + ((n_whole - 1) / NR) * NR * 8;  // end of the batched rounds
+  u32x4 wa[NR][2][VW], wb[NR][2][VW];
+
   // Round 0 on its own (the vocabulary is at least kSplitMinVocab, so all its groups are
   // whole): the part's bound is the k-th largest of its 512 first-round group maxima
-  // (every thread calls the selection; -inf values are not counted).
+  // (every thread calls the selection; -inf values are not counted).  The first batch's
+  // loads go out before the selection, whose barriers order only LDS.
   {
     u32x4 w[1][2][VW];
     load_rounds(0, w, std::integral_constant<int, 1>());
+    // (unconditional, so the load counts agree on every path; a load past the row
+    // returns 0 and is not used when there is no batch)
+    load_rounds(8, wa, nr);
     float x[2][8], gm[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -1283,7 +1313,7 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
       gk[e] = okey(gm[e]);
       if ((gk[e] >> kBinShift) < (uint32_t)kFirstFiniteBin) gk[e] = 0u;
     }
-    uint32_t kb = fine_bound<2>(L, gk, k);
+    uint32_t kb = fine_bound_inline<2>(L, gk, k);
     if (kb == 0u)  // the k largest spread over more than 256 bf16 steps
       kb = kth_key_call(L, gm[0], gm[1], -INFINITY, -INFINITY, -INFINITY, -INFINITY, -INFINITY,
                         -INFINITY, k);
@@ -1291,14 +1321,8 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
     if (t == 0 && kb == 0u) L.count = kCands + 1;  // cannot list: the combine searches
     do_round(0, w[0], gm, x);
   }
-  // The following rounds that are whole for every thread of the part run in batches of
-  // kSplitRounds, software-pipelined over two register sets: each batch's loads go out
-  // before the previous batch is computed, so a wave's arithmetic overlaps its own loads
-  // (the workgroups of all rows start together and would otherwise alternate between
-  // loading and computing in step).  That loop holds only the whole-round arithmetic;
-  // the rounds after it (at most a few) take do_round's per-group rules.
-  constexpr int NR = kSplitRounds;
-  const std::integral_constant<int, NR> nr;
+  // Whole-round arithmetic only (a branch in this loop, even a rare one, costs it about
+  // 40 registers): the groups whose maximum reaches the bound are noted as bits of hits.
   auto compute_whole = [&](int64_t cq0, const u32x4 (&w)[NR][2][VW]) {
 #pragma unroll
     for (int q = 0; q < NR; ++q) {
@@ -1316,38 +1340,55 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
       }
     }
   };
-  // rounds [8, c_whole) are whole for every thread of the part (its largest canonical
-  // thread is the binding one), in whole batches
-  const int64_t ct_max = (int64_t)p * kPartThreads + kPartThreads - 1;
-  const int64_t n_whole = G_whole > ct_max + 256 * 7 ? (G_whole - 1 - ct_max - 256 * 7) / 2048 + 1 : 0;
-  const int64_t c_whole = 8 + ((n_whole - 1) / NR) * NR * 8;  // end of the batched rounds
+  // wa holds rounds [8, 8 + 8 NR).  Every batch's loads are issued unconditionally (the
+  // batch after the last one holds the first rounds after the loop), so the load counts
+  // agree on every path and the wait before a batch's arithmetic leaves the next
+  // batch's loads in flight.
   int64_t c0 = 8;
   if (c_whole > 8) {
-    u32x4 wa[NR][2][VW], wb[NR][2][VW];
-    load_rounds(8, wa, nr);
     for (;;) {
-      const bool more_b = c0 + 8 * NR < c_whole;
-      if (more_b) load_rounds(c0 + 8 * NR, wb, nr);
+      load_rounds(c0 + 8 * NR, wb, nr);
       compute_whole(c0, wa);
       c0 += 8 * NR;
-      if (!more_b) break;
-      const bool more_a = c0 + 8 * NR < c_whole;
-      if (more_a) load_rounds(c0 + 8 * NR, wa, nr);
+      if (c0 >= c_whole) {
+#pragma unroll
+        for (int q = 0; q < NR; ++q)
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int h = 0; h < VW; ++h) wa[q][e][h] = wb[q][e][h];
+        break;
+      }
+      load_rounds(c0 + 8 * NR, wa, nr);
       compute_whole(c0, wb);
       c0 += 8 * NR;
-      if (!more_a) break;
+      if (c0 >= c_whole) break;
     }
   }
-  for (; (int64_t)ct + 256 * c0 < G; c0 += 8) {
+  // the rounds after the batches: the first NR from wa (loaded), the rest (if any) here
+#pragma unroll
+  for (int q = 0; q < NR; ++q) {
+    const int64_t cq = c0 + 8 * q;
+    if ((int64_t)ct + 256 * cq < G) {
+      float x[2][8], gm[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        unpack(wa[q][e], x[e]);
+        gm[e] = max8f(x[e]);
+      }
+      do_round(cq, wa[q], gm, x);
+    }
+  }
+  for (int64_t cq = c0 + 8 * NR; (int64_t)ct + 256 * cq < G; cq += 8) {
     u32x4 w[1][2][VW];
-    load_rounds(c0, w, std::integral_constant<int, 1>());
+    load_rounds(cq, w, std::integral_constant<int, 1>());
     float x[2][8], gm[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       unpack(w[0][e], x[e]);
       gm[e] = max8f(x[e]);
     }
-    do_round(c0, w[0], gm, x);
+    do_round(cq, w[0], gm, x);
   }
   // lane states and the part's maximum
   float* ls = a.lane_s + r * kLanes;

@@ -16,7 +16,7 @@
  * document, restated here from that specification:
  *   exp2(y): n = floor(y) saturated to int32 (NaN: INT32_MAX); f = min(fl(y - n),
  *            largest float < 1), 0 for an infinite or NaN y; P(f) = Horner-fma of
- *            the degree-5 polynomial with P(0) = 1 fitted to 2^f on [0, 1) for
+ *            the degree-4 polynomial with P(0) = 1 fitted to 2^f on [0, 1) for
  *            relative error (binary32 coefficients below); ldexp(P, n).
  *   weights: w(x) = exp2(fma(x, C, -(M*C))), C = log2(e) * (1/T).
  *   groups of 8 consecutive elements; lane (8t+i) owns groups t + 256*i + 2048*j.
@@ -38,8 +38,8 @@
 #define NL 2048
 
 static const float LOG2E = 0x1.715476p+0f;
-static const float POLY[6] = {0x1.0p+0f,      0x1.62e4bap-1f, 0x1.ebdb5ap-3f,
-                              0x1.c91ce4p-5f, 0x1.277854p-7f, 0x1.e974f6p-10f};
+static const float POLY[5] = {0x1.0p+0f, 0x1.62d6c2p-1f, 0x1.ee24b2p-3f, 0x1.abf636p-5f,
+                              0x1.b7fb26p-7f};
 
 float oc_exp2(float y) {
   float f;
@@ -53,8 +53,8 @@ float oc_exp2(float y) {
     if (f > 0x1.fffffep-1f) f = 0x1.fffffep-1f; /* fract is below 1 */
     n = fl >= 0x1p31f ? INT32_MAX : (fl < -0x1p31f ? INT32_MIN : (int)fl);
   }
-  float p = POLY[5];
-  for (int i = 4; i >= 0; --i) p = fmaf(p, f, POLY[i]);
+  float p = POLY[4];
+  for (int i = 3; i >= 0; --i) p = fmaf(p, f, POLY[i]);
   return ldexpf(p, n);
 }
 

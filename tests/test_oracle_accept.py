@@ -10,21 +10,28 @@ from oracle import accept as A
 
 
 # ---------------------------------------------------------------- exp2 / softmax
-def test_exp2_within_three_ulp_of_libm(oracle_lib):
-    # the polynomial's worst case on [0, 1) is 2.13 ulp, plus the rounding of y - floor(y)
+def test_exp2_within_3e6_of_libm(oracle_lib):
+    # the degree-4 polynomial's worst case on [0, 1) is 2.96e-6 relative (y - floor(y)
+    # and the ldexp are exact for these arguments); a dropped or perturbed coefficient
+    # moves it far beyond the bound
     ys = np.concatenate([np.linspace(-125.0, 0.0, 500001, dtype=np.float32),
                          np.float32(-np.random.default_rng(0).random(20000) * 30)])
     got = A.exp2_array(ys).astype(np.float64)
     ref = np.exp2(ys.astype(np.float64))
-    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
-    assert np.max(np.abs(got - ref) / ulp) <= 3.0
+    rel = np.abs(got - ref) / ref
+    assert rel.max() <= 3.0e-6
+    assert rel.max() >= 2.0e-6  # the fit's own error is reached: it is degree 4
+    # monotone in y across the integer steps of the argument
+    yy = np.sort(np.float32(-np.random.default_rng(5).random(200000) * 8))
+    assert np.all(np.diff(A.exp2_array(yy).astype(np.float64)) >= 0)
     assert A.exp2(0.0) == 1.0
     assert A.exp2(-1.0) == 0.5
     assert A.exp2(-300.0) == 0.0
     # no clamp: far below the float range, beyond int32 and -inf all underflow to 0
     assert A.exp2(-1e30) == 0.0 and A.exp2(-3e9) == 0.0 and A.exp2(float("-inf")) == 0.0
     # denormal results round like ldexp
-    assert A.exp2(-149.0) == 2.0 ** -149 and A.exp2(-127.5) == float(np.float32(2.0 ** -127.5))
+    assert A.exp2(-149.0) == 2.0 ** -149
+    assert A.exp2(-127.5) == float(np.ldexp(np.float32(A.exp2(0.5)), -128))
 
 
 @pytest.mark.parametrize("T", [1.0, 0.6, 1.7])
@@ -36,9 +43,9 @@ def test_softmax_close_to_float64(T):
     r /= r.sum(-1, keepdims=True)
     # C = log2(e)/T is a binary32 constant (relative error <= 1.5e-7), so the error of
     # an exponent grows with its distance from the row max: bound 2e-7 per bit of
-    # log2-distance plus a few ulp of exp2 and of the sum.
+    # log2-distance plus the exp2's 3e-6 (on the weight and on Z) and the sum's rounding.
     bits = -np.log2(r) + 1
-    assert np.all(np.abs(p - r) / r < 2e-7 * bits + 2e-6)
+    assert np.all(np.abs(p - r) / r < 2e-7 * bits + 8e-6)
 
 
 def test_row_stats_sum_matches_fsum():
@@ -47,7 +54,7 @@ def test_row_stats_sum_matches_fsum():
     assert M == x.max()
     c = np.float32(1 / math.log(2))
     w = np.exp2(x.astype(np.float64) * float(c) - float(M) * float(c))
-    assert abs(Z - math.fsum(w)) / math.fsum(w) < 2e-6
+    assert abs(Z - math.fsum(w)) / math.fsum(w) < 4e-6
 
 
 def test_row_stats_lanes_starting_at_minus_inf():
@@ -61,7 +68,7 @@ def test_row_stats_lanes_starting_at_minus_inf():
     assert M == fin.max()
     c = np.float32(1 / math.log(2))
     w = np.exp2(fin * float(c) - float(M) * float(c))
-    assert abs(Z - math.fsum(w)) / math.fsum(w) < 2e-6
+    assert abs(Z - math.fsum(w)) / math.fsum(w) < 4e-6
 
 
 @pytest.mark.parametrize("order", ["ascending", "descending"])
@@ -75,7 +82,7 @@ def test_row_stats_rescales_are_exact(order):
     c = np.float32(1 / math.log(2))
     w = np.exp2(x.astype(np.float64) * float(c) - float(M) * float(c))
     assert M == x.max()
-    assert abs(Z - math.fsum(w)) / math.fsum(w) < 2e-6
+    assert abs(Z - math.fsum(w)) / math.fsum(w) < 4e-6
 
 
 @pytest.mark.parametrize("scale", [1e3, 1e6, 1e8])
