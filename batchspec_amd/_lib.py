@@ -29,6 +29,7 @@ MASK_NONE = 0
 MASK_CAUSAL = 1
 MASK_TREE = 2
 MASK_STREAMING = 3
+MASK_CUSTOM = 4
 
 
 class AttnPlan(ctypes.Structure):
@@ -112,6 +113,7 @@ SIGNATURES = {
     "bsx_chain_speculative_sampling_logits": (c_int, [_P, _P, _P, c_int, c_float, _P, c_int, c_int,
                                                       c_int64, _P, _P, _P, _P, c_int64, _P]),
     "bsx_tree_masks": (c_int, [_P, c_int64, c_int, _P, c_int, _P, _P, _P]),
+    "bsx_custom_mask_prepare": (c_int, [_P, c_int64, _P, c_int, _P, _P, _P, _P]),
     "bsx_page_table_update": (c_int, [_P, _P, _P, _P, c_int32, c_int, c_int, c_int, c_int, _P, _P,
                                       _P, _P]),
     "bsx_accept_greedy_delete": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int64, c_int64, c_int,

@@ -8,11 +8,12 @@ batchspec/backends/mtp_engine.py:331-342,420-432,486-497) and runs it in every l
 constructor, ``plan`` and ``run``; the compute is the gfx950 kernel of
 ``libbsx.so``.
 
-Supported plan options: ``causal`` (bottom-right aligned), ``custom_mask`` whose
-prefix columns are all visible and whose last ``qo_len`` columns form an at most
-32-wide block (the MTP and EAGLE-tree masks), or the equivalent per-query-token
-``tree_mask_words``; and a StreamingLLM sink + window view (``sink_tokens``,
-``window_tokens``) for MagicDec-style draft attention.
+Supported plan options: ``causal`` (bottom-right aligned); ``custom_mask``, any
+flattened boolean mask of sum(qo_len * kv_len) entries, packed on the device (masks
+whose prefix columns are all visible and whose last ``qo_len`` columns form an at most
+32-wide block, the MTP and EAGLE-tree masks, take the fast tree path; others the general
+one); the equivalent per-query-token ``tree_mask_words``; and a StreamingLLM sink +
+window view (``sink_tokens``, ``window_tokens``) for MagicDec-style draft attention.
 """
 from __future__ import annotations
 
@@ -34,40 +35,6 @@ def _align(n: int) -> int:
 
 def _host_i32(t: torch.Tensor) -> np.ndarray:
     return np.ascontiguousarray(t.detach().to("cpu", torch.int32).numpy())
-
-
-def custom_mask_to_tree_words(custom_mask: torch.Tensor, qo_lens: np.ndarray,
-                              kv_lens: np.ndarray) -> np.ndarray:
-    """Flattened per-request bool masks [qo_len x kv_len] -> one uint32 per query token.
-
-    Bit c of the word of query token t is mask[t, kv_len - qo_len + c].  Raises
-    NotImplementedError unless every request attends to all of its first
-    kv_len - qo_len tokens and qo_len <= 32 (the layout of
-    batchspec/backends/mtp_engine.py:410-417).
-    """
-    m = custom_mask.detach().to("cpu", torch.bool).numpy().reshape(-1)
-    need = int(np.sum(qo_lens.astype(np.int64) * kv_lens.astype(np.int64)))
-    if m.size < need:
-        raise ValueError(f"custom_mask has {m.size} entries, the page table needs {need}")
-    words = np.zeros(int(qo_lens.sum()), dtype=np.uint32)
-    off = 0
-    row0 = 0
-    for q, kv in zip(qo_lens.tolist(), kv_lens.tolist()):
-        blk = m[off:off + q * kv].reshape(q, kv) if q > 0 else m[0:0].reshape(0, kv)
-        off += q * kv
-        if q == 0:
-            continue
-        if q > 32 or kv < q:
-            raise NotImplementedError(
-                "custom masks are supported when qo_len <= 32 <= kv_len pattern holds "
-                f"(got qo_len={q}, kv_len={kv})")
-        if not blk[:, :kv - q].all():
-            raise NotImplementedError(
-                "custom masks must attend to every prefix token (kv_len - qo_len columns)")
-        tail = blk[:, kv - q:].astype(np.uint64)
-        words[row0:row0 + q] = (tail << np.arange(q, dtype=np.uint64)).sum(axis=1).astype(np.uint32)
-        row0 += q
-    return words
 
 
 class BatchPrefillWithPagedKVCacheWrapper:
@@ -102,6 +69,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._plan: Optional[_lib.AttnPlan] = None
         self._kv_indices: Optional[torch.Tensor] = None
         self._mask_words: Optional[torch.Tensor] = None
+        self._custom_desc: Optional[torch.Tensor] = None  # packed general custom mask
         self._blob_bytes = 0
         self._pinned: Optional[torch.Tensor] = None
         self._pinned_tab: Optional[torch.Tensor] = None
@@ -151,7 +119,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         with page-table lengths that change between replays.  ``max_qo_len`` bounds
         every request's query tokens; q and out then need ``batch * max_qo_len`` token
         rows.  Masks: causal, sink+window, or ``tree_mask_words`` (device tensor, one
-        word per token row); a boolean ``custom_mask`` needs the host path.
+        word per token row); a boolean ``custom_mask`` needs a host plan.
         Malformed tables are reported by :meth:`device_plan_error`, not raised.
         """
         if head_dim_vo is not None and head_dim_vo != head_dim_qk:
@@ -187,6 +155,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
 
         streaming = sink_tokens > 0 or window_tokens > 0
         words = None
+        packed = None
         if tree_mask_words is not None or custom_mask is not None:
             if causal or streaming:
                 raise ValueError("custom/tree mask cannot be combined with causal or streaming")
@@ -197,7 +166,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
                 qo_lens = np.diff(qo_h)
                 npages = np.diff(kvp_h)
                 kv_lens = np.where(npages > 0, (npages - 1) * page_size + last_h, 0)
-                words = custom_mask_to_tree_words(custom_mask, qo_lens, kv_lens)
+                packed = self._pack_custom_mask(custom_mask, qo_h, qo_lens, kv_lens)
+                mode, words = packed[0], packed[2]
         elif streaming:
             mode = _lib.MASK_STREAMING
         elif causal:
@@ -269,8 +239,57 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._set_kv_indices(paged_kv_indices, non_blocking)
         if words is not None:
             self._set_mask_words(words, int(plan.total_qo))
+        if packed is not None:
+            self._custom_desc = packed[1]
         self._plan = plan
         self._dtype = qdt
+
+    def _pack_custom_mask(self, custom_mask: torch.Tensor, qo_h: np.ndarray, qo_lens: np.ndarray,
+                          kv_lens: np.ndarray):
+        """plan(custom_mask=...) as FlashInfer's plan() takes it (the MTP engine's call at
+        batchspec/backends/mtp_engine.py:399-432): the flattened boolean mask of
+        sum(qo_len * kv_len) entries, packed into bits on the device
+        (bsx_custom_mask_prepare).  Returns (mask mode, descriptor, tree words):
+        BSX_MASK_TREE with one word per query token when every request's mask sees its
+        prefix and has at most 32 query tokens; else BSX_MASK_CUSTOM with the packed bits.
+        One host read of the per-request verdicts (a few bytes), no copy of the mask."""
+        dev = self._device
+        batch = int(qo_lens.shape[0])
+        need = int(np.sum(qo_lens.astype(np.int64) * kv_lens.astype(np.int64)))
+        m = custom_mask.reshape(-1)
+        if m.numel() < need:
+            raise ValueError(f"custom_mask has {m.numel()} entries, the page table needs {need}")
+        if need >= 2 ** 31:
+            raise NotImplementedError("custom masks of 2^31 entries or more")
+        if m.device != dev:
+            m = m.to(dev)
+        if m.dtype != torch.bool:
+            m = m != 0
+        m = m.contiguous()
+        off = np.zeros(batch, np.int64)
+        if batch > 1:
+            off[1:] = np.cumsum(qo_lens.astype(np.int64) * kv_lens.astype(np.int64))[:-1]
+        req = np.stack([qo_h[:-1].astype(np.int64), qo_lens, kv_lens, off], 1).astype(np.int32)
+        total_qo = int(qo_h[-1])
+        tree = torch.empty(max(total_qo, 1), dtype=torch.int32, device=dev)
+        desc = torch.empty(batch + (need + 31) // 32 + 1, dtype=torch.int32, device=dev)
+        general = torch.empty(max(batch, 1), dtype=torch.int32, device=dev)
+        with torch.cuda.device(dev):
+            req_d = torch.from_numpy(req).to(dev)
+            rc = _lib.load().bsx_custom_mask_prepare(m.data_ptr(), need, req_d.data_ptr(), batch,
+                                                     desc.data_ptr(), tree.data_ptr(),
+                                                     general.data_ptr(), stream_of(dev))
+            _lib.check(rc, "BatchPrefillWithPagedKVCacheWrapper.plan(custom_mask)")
+            verdict = general[:batch].cpu().numpy()
+        if np.any(verdict == 2):
+            raise ValueError("custom_mask entries of a request lie outside the mask")
+        if np.any(verdict == 1):
+            if self._use_cuda_graph:
+                raise NotImplementedError(
+                    "graph-mode plans take custom masks whose rows see every prefix token "
+                    "and that have at most 32 query tokens per request")
+            return _lib.MASK_CUSTOM, desc, None
+        return _lib.MASK_TREE, None, tree[:total_qo]
 
     def _host_tables(self, *tables: torch.Tensor) -> list:
         """Host int32 copies of the page-table arrays the host planner reads.  Device
@@ -371,10 +390,14 @@ class BatchPrefillWithPagedKVCacheWrapper:
         if w.numel() < rows:
             raise ValueError("tree_mask_words needs one word per query token")
         w = w.reshape(-1)[:rows]
-        if self._mask_words is None or self._mask_words.numel() < w.numel():
+        self._mask_buffer(w.numel())[: w.numel()].copy_(w, non_blocking=True)
+
+    def _mask_buffer(self, rows: int) -> torch.Tensor:
+        """The per-token mask-word buffer, at least `rows` words (fixed in graph mode)."""
+        if self._mask_words is None or self._mask_words.numel() < rows:
             if self._use_cuda_graph and self._mask_words is not None:
                 raise ValueError("mask grew beyond its cuda-graph buffer")
-            cap = max(w.numel(), 1)
+            cap = max(rows, 1)
             if self._use_cuda_graph and self._qo_indptr_buf is not None:
                 cap = max(cap, 32 * (self._qo_indptr_buf.numel()))
             cmb = self._custom_mask_buf
@@ -386,7 +409,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
                 self._mask_words = cmb.view(torch.uint8).reshape(-1)[: 4 * cap].view(torch.int32)
             else:
                 self._mask_words = torch.zeros(cap, dtype=torch.int32, device=self._device)
-        self._mask_words[: w.numel()].copy_(w, non_blocking=True)
+        return self._mask_words
 
     def _plan_on_device(self, qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len,
                         num_qo_heads, num_kv_heads, head_dim, page_size, custom_mask, causal,
@@ -499,8 +522,11 @@ class BatchPrefillWithPagedKVCacheWrapper:
         blob = ws[: int(plan.plan_ints) * 4]
         fws = ws[self._blob_bytes:] if int(plan.float_ws_bytes) > 0 else None
         lib = _lib.load()
-        mw = (None if self._mask_words is None or plan.mask_mode != _lib.MASK_TREE
-              else self._mask_words.data_ptr())
+        if plan.mask_mode == _lib.MASK_CUSTOM:
+            mw = self._custom_desc.data_ptr()
+        else:
+            mw = (None if self._mask_words is None or plan.mask_mode != _lib.MASK_TREE
+                  else self._mask_words.data_ptr())
         if append_key is None and append_value is None:
             rc = lib.bsx_attn_run(ctypes.byref(plan), blob.data_ptr(),
                                   None if fws is None else fws.data_ptr(),

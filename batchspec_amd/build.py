@@ -42,6 +42,7 @@ HIP_SOURCES = {
     "page_table.hip": [],
     "plan_device.hip": [],
     "probe.hip": [],
+    "custom_mask.hip": [],
     "accept.hip": ["-ffp-contract=off"],
     "filter.hip": ["-ffp-contract=off"],
 }

@@ -56,7 +56,10 @@ struct Params {
   const char* v_cache;
   int64_t page_stride_bytes;
   const int32_t* kv_indices;
+  // BSX_MASK_TREE: one word per query token.  BSX_MASK_CUSTOM: [batch] bit offsets of
+  // the requests' masks, then the packed bits (bit f at word bits_base + f / 32).
   const uint32_t* mask_words;
+  int bits_base;
   uint16_t* out;
   int64_t out_stride;
   float* lse_out;
@@ -420,8 +423,35 @@ __device__ void append_rows_of_segments(const Params& p, int seg_begin, int seg_
   __syncthreads();
 }
 
-// NT: query-row tiles of 16 per wave.  D: head dim (64 or 128).
-template <int DT, int D, int NT, bool PS_GE16>
+// 32 bits of a packed custom mask starting at bit f (the bits end with a padding word).
+__device__ __forceinline__ uint32_t mask_bits_at(const uint32_t* bits, int64_t f) {
+  const int64_t w = f >> 5;
+  const uint64_t pair = ((uint64_t)bits[w + 1] << 32) | bits[w];
+  return (uint32_t)(pair >> (f & 31));
+}
+
+// General custom mask: token j0 + 16 st + 4 g4 + e of a lane's query row is visible iff
+// bit (16 st + 4 g4 + e) of the row's tile word tw[nt] is set (and j <= lim, the kv end).
+template <int NT>
+__device__ __forceinline__ void mask_tile_bits(f32x4 (&sacc)[2][NT], const RowMask (&rm)[NT],
+                                               const uint32_t (&tw)[NT], int j0, int g4) {
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = 16 * st + 4 * g4 + e;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const bool vis = (j0 + c <= rm[nt].lim) & (((tw[nt] >> c) & 1u) != 0u);
+        sacc[st][nt][e] = vis ? sacc[st][nt][e] : -INFINITY;
+      }
+    }
+}
+
+// NT: query-row tiles of 16 per wave.  D: head dim (64 or 128).  CUSTOM: a general
+// boolean mask (BSX_MASK_CUSTOM): every tile is masked, with the 32 bits of each query
+// row's mask over the tile read at the start of its step.
+template <int DT, int D, int NT, bool PS_GE16, bool CUSTOM = false>
 __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
   constexpr int KS = D / 32;  // k-steps of the QK^T contraction
   constexpr int NJ = D / 16;  // output d tiles (also d values per lane in V loads)
@@ -550,12 +580,16 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
     const int win_beg = p.mask_mode == BSX_MASK_STREAMING ? cur.kv_len - p.window : cur.kv_len;
     RowMask rm[NT];
     row_masks<NT>(p, cur, row0, c16, rm);
+    int64_t mrow[NT];  // CUSTOM: bit offset of each lane row's mask row
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int row = row0 + nt * 16 + c16;
       const bool rv = row < nrows;
       const int tq = rv ? row / g : 0;
       const int hh = rv ? row - tq * g : 0;
+      if constexpr (CUSTOM)
+        mrow[nt] = (int64_t)ld_uniform(reinterpret_cast<const int32_t*>(p.mask_words), cur.b) +
+                   (int64_t)tq * cur.kv_len;
       if (has_tiles) {
         const uint16_t* qp =
             p.q + (int64_t)(cur.qo_start + tq) * p.q_stride + (int64_t)(h * g + hh) * D;
@@ -600,6 +634,12 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       // letting them be hoisted into registers the pipelined tiles need.
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
+      // (CUSTOM: every tile is masked; its mask bits load with the tile's scores)
+      uint32_t tw[NT];
+      if constexpr (CUSTOM) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) tw[nt] = mask_bits_at(p.mask_words + p.bits_base, mrow[nt] + j0);
+      }
 
       f32x4 sacc[2][NT];
 #pragma unroll
@@ -619,12 +659,15 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (PREFETCH) load_tile_k(pf_tile, pf_kv, pf_pages);
 
-      if constexpr (MASKED) mask_tile<NT>(sacc, rm, j0, g4, diag, sink_end, win_beg);
+      if constexpr (CUSTOM)
+        mask_tile_bits<NT>(sacc, rm, tw, j0, g4);
+      else if constexpr (MASKED)
+        mask_tile<NT>(sacc, rm, j0, g4, diag, sink_end, win_beg);
 
       uint32_t pb[NT][4];
       softmax_tile<DT, NJ, NT>(sacc, p.scale_log2, m_ref, l_run, o, pb);
 
-      if constexpr (MASKED) zero_rows_past_end<VW>(vraw, j0, g4, cur.kv_len);
+      if constexpr (MASKED || CUSTOM) zero_rows_past_end<VW>(vraw, j0, g4, cur.kv_len);
       u32x4 va[NJ];
       transpose_v<NJ, VW>(vraw, va);
       // The transposed operands must be complete before the V registers are refilled:
@@ -641,7 +684,7 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       // Tiles [t0, t_split) lie entirely inside the visible prefix (no mask needed);
       // [t_split, t1) touch the draft block, the kv end, or the sink/window view.
       int limit = p.mask_mode == BSX_MASK_NONE ? cur.kv_len : diag;
-      if (p.mask_mode == BSX_MASK_STREAMING) limit = 0;
+      if (p.mask_mode == BSX_MASK_STREAMING || CUSTOM) limit = 0;
       // The last tile of the workgroup's schedule has nothing to prefetch: it runs
       // after the loops (masked form, valid for any tile).
       const int t_end = has_next ? cur.t1 : cur.t1 - 1;
@@ -1072,7 +1115,11 @@ __global__ void __launch_bounds__(256) empty_kernel(Params p, int total_qo) {
 template <int DT, int D, int NT, bool PS16>
 static int launch_main(const bsx_attn_plan_t* plan, const Params& prm, int waves, hipStream_t st) {
   dim3 grid(plan->num_ctas, (plan->num_kv_heads / plan->heads_per_cta) * prm.n_qgroups);
-  hipLaunchKernelGGL((verify_attn_kernel<DT, D, NT, PS16>), grid, dim3(64 * waves), 0, st, prm);
+  if (plan->mask_mode == BSX_MASK_CUSTOM)
+    hipLaunchKernelGGL((verify_attn_kernel<DT, D, NT, PS16, true>), grid, dim3(64 * waves), 0, st,
+                       prm);
+  else
+    hipLaunchKernelGGL((verify_attn_kernel<DT, D, NT, PS16>), grid, dim3(64 * waves), 0, st, prm);
   BSX_LAUNCH_CHECK();
   return BSX_OK;
 }
@@ -1138,8 +1185,11 @@ static int attn_run_impl(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d
               "verify attention supports bf16 and fp16 (got dtype %d)", dtype);
   BSX_REQUIRE(plan->head_dim == 64 || plan->head_dim == 128, BSX_ERR_UNSUPPORTED,
               "head_dim %d not supported (64 or 128)", plan->head_dim);
-  BSX_REQUIRE(plan->mask_mode != BSX_MASK_TREE || mask_words_d != nullptr, BSX_ERR_INVALID,
-              "tree mask mode needs mask words");
+  BSX_REQUIRE((plan->mask_mode != BSX_MASK_TREE && plan->mask_mode != BSX_MASK_CUSTOM) ||
+                  mask_words_d != nullptr,
+              BSX_ERR_INVALID, "tree and custom mask modes need mask words");
+  BSX_REQUIRE(plan->mask_mode != BSX_MASK_CUSTOM || !plan->shared_kv_tiles, BSX_ERR_INVALID,
+              "inconsistent plan (custom masks run on the per-wave kernel)");
   BSX_REQUIRE(plan->num_partials == 0 || float_ws_d != nullptr, BSX_ERR_INVALID,
               "plan splits sequences but no float workspace given");
   BSX_REQUIRE(q_stride_tok >= (int64_t)plan->num_qo_heads * plan->head_dim &&
@@ -1194,6 +1244,7 @@ static int attn_run_impl(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d
   prm.page_stride_bytes = page_stride * 2;
   prm.kv_indices = kv_indices_d;
   prm.mask_words = mask_words_d;
+  prm.bits_base = plan->batch;
   prm.out = static_cast<uint16_t*>(out_d);
   prm.out_stride = out_stride_tok;
   prm.lse_out = lse_d;

@@ -102,7 +102,7 @@ struct GridShape {
 };
 
 static GridShape grid_shape(int max_qo, int group, int num_kv_heads, int head_dim, int page_size,
-                     int num_cus) {
+                     int num_cus, int mask_mode) {
   GridShape g;
   // Query rows per kv head = qo_len * group.  A wave covers 16 or 32 of them.
   const int64_t max_rows = (int64_t)max_qo * group;
@@ -110,7 +110,8 @@ static GridShape grid_shape(int max_qo, int group, int num_kv_heads, int head_di
   g.qrow_blocks = (int)std::max<int64_t>(1, (max_rows + g.qrow_tile - 1) / g.qrow_tile);
   // Several waves per kv head: they share each K/V tile through LDS when a 16-token
   // subtile always lies inside one page (the shared kernel's loads assume it).
-  g.shared = g.qrow_blocks > 1 && page_size >= 16;
+  // (a general custom mask runs on the per-wave kernel, which reads the mask bits)
+  g.shared = g.qrow_blocks > 1 && page_size >= 16 && mask_mode != BSX_MASK_CUSTOM;
   g.hpc = 1;  // kv heads per workgroup: largest divisor of num_kv_heads that fits
   if (g.shared) {
     g.qbpc = g.qrow_blocks <= 2 ? 2 : g.qrow_blocks <= 4 ? 4 : 8;
@@ -305,7 +306,7 @@ static void write_blob(const HostSchedule& hs, const int32_t* qo_indptr_h,
                "head_dim %d not supported (64 or 128)", head_dim);                              \
   PLAN_REQUIRE(page_size >= 1 && page_size <= 1024 && (page_size & (page_size - 1)) == 0,       \
                BSX_ERR_UNSUPPORTED, "page_size %d must be a power of two <= 1024", page_size);  \
-  PLAN_REQUIRE(mask_mode >= BSX_MASK_NONE && mask_mode <= BSX_MASK_STREAMING, BSX_ERR_INVALID,  \
+  PLAN_REQUIRE(mask_mode >= BSX_MASK_NONE && mask_mode <= BSX_MASK_CUSTOM, BSX_ERR_INVALID,     \
                "unknown mask mode %d", mask_mode);                                              \
   PLAN_REQUIRE(num_cus >= 1, BSX_ERR_INVALID, "num_cus must be >= 1");                          \
   PLAN_REQUIRE(mask_mode != BSX_MASK_STREAMING || (sink_tokens >= 0 && window_tokens >= 0),     \
@@ -327,7 +328,8 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
                           mask_mode, kv_indices_len, &hs);
   if (rc != BSX_OK) return rc;
   const int group = num_qo_heads / num_kv_heads;
-  const GridShape gs = grid_shape(hs.max_qo, group, num_kv_heads, head_dim, page_size, num_cus);
+  const GridShape gs =
+      grid_shape(hs.max_qo, group, num_kv_heads, head_dim, page_size, num_cus, mask_mode);
   schedule(batch, mask_mode, sink_tokens, window_tokens, gs.num_ctas, &hs);
   const int W = (int)hs.per_cta.size();
   const int nseg = hs.nseg;
@@ -459,7 +461,8 @@ extern "C" int bsx_attn_plan_device_shape(int batch, int num_qo_heads, int num_k
   PLAN_REQUIRE(mask_mode != BSX_MASK_TREE || max_qo_len <= 32, BSX_ERR_UNSUPPORTED,
                "tree mask supports at most 32 query tokens per request");
   const int group = num_qo_heads / num_kv_heads;
-  const GridShape gs = grid_shape(max_qo_len, group, num_kv_heads, head_dim, page_size, num_cus);
+  const GridShape gs =
+      grid_shape(max_qo_len, group, num_kv_heads, head_dim, page_size, num_cus, mask_mode);
   const int W = gs.num_ctas;
   PLAN_REQUIRE(W <= bsx::attn_shape::kMaxDevicePlanCtas, BSX_ERR_UNSUPPORTED,
                "grid of %d workgroups too large for a device plan", W);

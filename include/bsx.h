@@ -50,9 +50,11 @@ enum {
   BSX_MASK_TREE = 2,   /* full attention to the first kv_len - qo_len tokens,
                           then bit (j - (kv_len - qo_len)) of a per-query-token
                           uint32 word over the last qo_len tokens (qo_len <= 32) */
-  BSX_MASK_STREAMING = 3 /* sink + recent window view: token j is visible iff
+  BSX_MASK_STREAMING = 3, /* sink + recent window view: token j is visible iff
                           j < sink or j >= kv_len - window, combined with the
                           causal rule over the last qo_len tokens              */
+  BSX_MASK_CUSTOM = 4  /* any boolean [qo_len x kv_len] mask per request, packed
+                          by bsx_custom_mask_prepare (host plans, per-wave kernel) */
 };
 
 const char* bsx_last_error(void);
@@ -181,7 +183,8 @@ int bsx_attn_plan_device(const bsx_attn_plan_t* plan, const int32_t* qo_indptr_d
  *   v_cache_d  same addressing (for the reference layout [P,2,ps,H,D],
  *              v_cache_d = k_cache_d + ps*H*D and page_stride = 2*ps*H*D)
  *   kv_indices_d page ids in CSR order (paged_kv_indices)
- *   mask_words_d uint32 per query token for BSX_MASK_TREE, else NULL
+ *   mask_words_d uint32 per query token for BSX_MASK_TREE; the descriptor of
+ *              bsx_custom_mask_prepare for BSX_MASK_CUSTOM; else NULL
  *   out_d      [total_qo, num_qo_heads, head_dim], same dtype as q
  *   lse_d      optional float [total_qo, num_qo_heads] log-sum-exp (natural
  *              log, of the scaled scores), or NULL
@@ -213,6 +216,26 @@ int bsx_attn_run_append(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d,
                         void* out_d, int64_t out_stride_tok, float* lse_d,
                         const void* k_new_d, int64_t k_new_stride_tok, const void* v_new_d,
                         int64_t v_new_stride_tok, void* stream);
+
+/* plan(custom_mask=...) as the MTP engine calls it (batchspec/backends/mtp_engine.py:
+ * 399-432: the flattened boolean mask, per request cat(ones(qo_len, cachelen),
+ * common_attn_mask), qo_len x kv_len entries), packed on the device as FlashInfer's
+ * plan() packs it.  mask_d: n_bools bytes (0 = hidden).  req_d [batch][4] int32 =
+ * (qo_start, qo_len, kv_len, offset of the request's first entry in mask_d).  Writes
+ *   desc_d       batch + ceil(n_bools / 32) + 1 uint32: the bit offsets, then the
+ *                packed bits (little bit order) and a padding word: the mask_words_d
+ *                of a BSX_MASK_CUSTOM run;
+ *   general_d    [batch] int32: 0 when the request's mask has the tree form (every row
+ *                sees its first kv_len - qo_len tokens, qo_len <= 32), 1 otherwise, 2
+ *                when its entries do not lie inside the mask;
+ *   tree_words_d [total_qo] uint32, for the requests of the tree form: the
+ *                mask_words_d of a BSX_MASK_TREE run (bit c of token i = entry
+ *                (i, kv_len - qo_len + c)).
+ * A batch whose requests all have the tree form runs as BSX_MASK_TREE (the fast
+ * path); otherwise as BSX_MASK_CUSTOM.  Two launches, no host synchronisation. */
+int bsx_custom_mask_prepare(const void* mask_d, int64_t n_bools, const int32_t* req_d,
+                            int batch, uint32_t* desc_d, uint32_t* tree_words_d,
+                            int32_t* general_d, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* 2. Paged KV append                                                         */

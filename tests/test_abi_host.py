@@ -12,7 +12,6 @@ import torch
 
 import batchspec_amd as bsx
 from batchspec_amd import _lib, masks
-from batchspec_amd.attention import custom_mask_to_tree_words
 from oracle import masks as OM
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -139,6 +138,28 @@ def test_plan_streaming_skips_middle_tiles():
     assert tiles == list(range(0, 2)) + list(range((kv - 512) // 32, -(-kv // 32)))
 
 
+def test_plan_custom_masks_cover_every_tile_on_the_per_wave_kernel():
+    # 25 query tokens x group 4 = 100 rows: the tree mode takes the shared-tile kernel,
+    # a general custom mask the per-wave one (it reads mask bits per row); every tile of
+    # every request is scheduled either way, and the custom mode accepts qo_len > 32
+    qo = np.array([0, 25, 50, 90])
+    kv = np.array([300, 2000, 1000])
+    kvp = np.concatenate([[0], np.cumsum(-(-kv // 16))])
+    last = (kv - 1) % 16 + 1
+    with pytest.raises(NotImplementedError, match="tree mask"):
+        _plan(qo, kvp, last, mode=_lib.MASK_TREE)
+    pt, _ = _plan(qo[:3], kvp[:3], last[:2], mode=_lib.MASK_TREE)
+    assert pt.shared_kv_tiles == 1
+    pc, blob = _plan(qo, kvp, last, mode=_lib.MASK_CUSTOM)
+    assert pc.shared_kv_tiles == 0 and pc.mask_mode == _lib.MASK_CUSTOM
+    segs, _ = _segments(pc, blob)
+    for b in range(3):
+        tiles = sorted(t for s in segs if s[0] == b for t in range(s[1], s[2]))
+        assert tiles == list(range(-(-int(kv[b]) // 32)))
+    with pytest.raises(ValueError, match="unknown mask mode"):
+        _plan(qo, kvp, last, mode=5)
+
+
 @pytest.mark.parametrize("bad,exc", [
     (dict(D=96), NotImplementedError),
     (dict(Hq=30, Hkv=8), ValueError),
@@ -188,21 +209,6 @@ def test_mtp_parents_give_the_mtp_mask(k):
     np.testing.assert_array_equal(m, rm)
     np.testing.assert_array_equal(depth, rpos)
     assert np.all(par < np.arange(par.size))
-
-
-def test_custom_mask_packing_of_mtp_verify_mask():
-    k = 4
-    cachelens = [7, 0, 30]
-    flat = masks.mtp_verify_custom_mask(cachelens, k)
-    S = (k + 1) ** 2
-    words = custom_mask_to_tree_words(flat, np.full(3, S), np.array(cachelens) + S)
-    common, _ = masks.mtp_attn_mask_and_position_ids(k)
-    expect = np.tile(masks.mask_to_words(common), 3)
-    np.testing.assert_array_equal(words, expect)
-    bad = flat.clone()
-    bad[3] = False  # hide a prefix token of request 0
-    with pytest.raises(NotImplementedError):
-        custom_mask_to_tree_words(bad, np.full(3, S), np.array(cachelens) + S)
 
 
 def test_product_has_no_cpu_path():
