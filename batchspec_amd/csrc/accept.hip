@@ -802,7 +802,7 @@ __global__ void __launch_bounds__(pt::kThreads) greedy_eval_delete_kernel(
       s_acc[b] = n + 1;
     }
   }
-  __syncthreads();
+  lds_barrier();  // (s_acc; the output stores need not land first)
   pt::update_pages(pa, [&](int r) -> int32_t { return n_inserted - s_acc[r]; });
 }
 

@@ -116,4 +116,12 @@ __device__ __forceinline__ uint16_t f32_to_half_bits(float f) {
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Workgroup barrier that orders LDS only (s_waitcnt lgkmcnt(0); s_barrier): unlike
+// __syncthreads it does not wait for the global loads and stores in flight, so a barrier
+// that follows global stores read only by later kernels (lists, lane states, records,
+// page-table arrays) does not pay their round trip.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 }  // namespace bsx

@@ -489,9 +489,9 @@ __device__ __forceinline__ bool walk(RowsLds& L, int n, float c, float neg, bool
       }
     }
   }
-  __syncthreads();
+  lds_barrier();  // (the list stores need not land first)
   if (t == 0 && (list_out == nullptr || L.nk > kCap)) L.nk = -1;
-  __syncthreads();
+  lds_barrier();
   return true;
 }
 
@@ -1096,11 +1096,8 @@ struct SplitArgs {
 // k of the keys are at or above it, and it is within one bf16 step of the k-th largest.
 // Returns 0 when the k largest do not fit the 256 bins (or there are fewer than k).
 // Every thread calls it; uses hist, part and bin of L.  Its barriers order only LDS
-// (s_waitcnt lgkmcnt(0); s_barrier): global loads the caller has in flight stay in
-// flight across it when it is inlined (fine_bound_inline).
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
+// (lds_barrier): global loads the caller has in flight stay in flight across it when it
+// is inlined (fine_bound_inline).
 
 template <int N>
 __device__ __forceinline__ uint32_t fine_bound_inline(RowsLds& L, const uint32_t (&key)[N],
@@ -1406,7 +1403,7 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
   // read again one per thread: a single round trip, where a thread reading its own noted
   // groups in turn would put several dependent ones on the workgroup's tail.
   if (t == 0) L.ng = 0;
-  __syncthreads();
+  lds_barrier();  // (the lane-state stores need not land first)
   uint32_t hb = hits;
 #pragma unroll 1
   while (hb != 0u) {
@@ -1479,7 +1476,7 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
           }
         }
     }
-    __syncthreads();
+    lds_barrier();  // (the key stores need not land first)
     if (kb != 0u && L.nk <= kPartList) {
       po.kb = kb;
       po.count = L.nk;

@@ -41,6 +41,7 @@ __device__ __forceinline__ void update_pages(const Args& a, Delta delta) {
   __shared__ int32_t s_scan[kThreads];
   __shared__ int32_t s_pages[kThreads];
   __shared__ int32_t s_wave[kThreads / 64];
+  __shared__ int32_t s_flag[2][kThreads / 64];
   __shared__ int32_t s_base;
   const int t = threadIdx.x;
   const int ps = a.page_size;
@@ -56,8 +57,21 @@ __device__ __forceinline__ void update_pages(const Args& a, Delta delta) {
       over |= pages > a.max_pages;
     }
   }
-  any_pos = __syncthreads_or(any_pos);
-  over = __syncthreads_or(over);
+  // (per-wave flags through LDS: no wait for global stores the caller has in flight)
+  const bool wpos = __builtin_amdgcn_ballot_w64(any_pos != 0) != 0ull;
+  const bool wover = __builtin_amdgcn_ballot_w64(over != 0) != 0ull;
+  if ((t & 63) == 0) {
+    s_flag[0][t >> 6] = wpos ? 1 : 0;
+    s_flag[1][t >> 6] = wover ? 1 : 0;
+  }
+  lds_barrier();
+  any_pos = 0;
+  over = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) {
+    any_pos |= s_flag[0][w];
+    over |= s_flag[1][w];
+  }
   if (!any_pos) return;
   if (over) {
     if (t == 0 && a.errors) a.errors[0] += 1;
@@ -81,12 +95,13 @@ __device__ __forceinline__ void update_pages(const Args& a, Delta delta) {
       a.cachelens[r] = cl > 0 ? (int32_t)cl : 0;
     }
   }
-  __syncthreads();
 
   // indptr (exclusive scan of the page counts) and indices, kThreads requests at a
-  // time; each chunk's counts and starts stay in LDS for the index writes
+  // time; each chunk's counts and starts stay in LDS for the index writes.  A thread
+  // reads back only the counts it wrote itself (request r0 + t), so the barriers here
+  // order LDS only and never wait for the global stores in flight.
   if (t == 0) s_base = 0;
-  __syncthreads();
+  lds_barrier();
   for (int r0 = 0; r0 < a.B; r0 += kThreads) {
     const int r = r0 + t;
     const int32_t v = r < a.B ? a.num_pages[r] : 0;
@@ -100,7 +115,7 @@ __device__ __forceinline__ void update_pages(const Args& a, Delta delta) {
       if (lane >= d) x += o;
     }
     if (lane == 63) s_wave[wave] = x;
-    __syncthreads();
+    lds_barrier();
     if (t < 64) {
       int32_t w = t < kThreads / 64 ? s_wave[t] : 0;
 #pragma unroll
@@ -110,9 +125,9 @@ __device__ __forceinline__ void update_pages(const Args& a, Delta delta) {
       }
       if (t < kThreads / 64) s_wave[t] = w;  // inclusive over waves
     }
-    __syncthreads();
+    lds_barrier();
     s_scan[t] = x + (wave > 0 ? s_wave[wave - 1] : 0);
-    __syncthreads();
+    lds_barrier();
     const int32_t base = s_base;
     if (r < a.B) a.indptr[r] = base + s_scan[t] - v;
     const int nr = min(kThreads, a.B - r0);
@@ -122,9 +137,9 @@ __device__ __forceinline__ void update_pages(const Args& a, Delta delta) {
       const int32_t beg = base + s_scan[q] - n;
       for (int k = t; k < n; k += kThreads) a.indices[beg + k] = (r0 + q) * a.max_pages + k;
     }
-    __syncthreads();
+    lds_barrier();
     if (t == kThreads - 1) s_base = base + s_scan[t];
-    __syncthreads();
+    lds_barrier();
   }
   if (t == 0) a.indptr[a.B] = s_base;
 }
