@@ -518,6 +518,11 @@ class BatchPrefillWithPagedKVCacheWrapper:
                                 or lse.shape[0] < plan.total_qo):
             raise ValueError(f"lse must be a contiguous float32 tensor of at least "
                              f"[{plan.total_qo}, {plan.num_qo_heads}]")
+        if append_key is not None or append_value is not None:
+            kn = _append_rows(append_key, "append_key", q, plan, k_cache.dtype)
+            vn = _append_rows(append_value, "append_value", q, plan, k_cache.dtype)
+        if q.shape[0] == 0:  # no query token: nothing to attend or to append
+            return (out, lse) if return_lse else out
         ws = self._ws
         blob = ws[: int(plan.plan_ints) * 4]
         fws = ws[self._blob_bytes:] if int(plan.float_ws_bytes) > 0 else None
@@ -535,8 +540,6 @@ class BatchPrefillWithPagedKVCacheWrapper:
                                   self._kv_indices.data_ptr(), mw,
                                   out.data_ptr(), out.stride(0), _lib.ptr(lse), stream_of(dev))
         else:
-            kn = _append_rows(append_key, "append_key", q, plan, k_cache.dtype)
-            vn = _append_rows(append_value, "append_value", q, plan, k_cache.dtype)
             rc = lib.bsx_attn_run_append(ctypes.byref(plan), blob.data_ptr(),
                                          None if fws is None else fws.data_ptr(),
                                          dtype_code(q.dtype), q.data_ptr(), q.stride(0),
