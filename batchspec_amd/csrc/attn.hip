@@ -423,11 +423,16 @@ __device__ void append_rows_of_segments(const Params& p, int seg_begin, int seg_
   __syncthreads();
 }
 
-// 32 bits of a packed custom mask starting at bit f (the bits end with a padding word).
-__device__ __forceinline__ uint32_t mask_bits_at(const uint32_t* bits, int64_t f) {
-  const int64_t w = f >> 5;
-  const uint64_t pair = ((uint64_t)bits[w + 1] << 32) | bits[w];
-  return (uint32_t)(pair >> (f & 31));
+// Packed custom mask bits: the two words holding bits [f, f + 32) (the bits end with a
+// padding word), from one 8-byte load (dword alignment is enough for it); the 32 bits
+// are the pair shifted right by f mod 32.
+typedef uint32_t u32x2_dw __attribute__((ext_vector_type(2), aligned(4)));
+__device__ __forceinline__ u32x2 mask_pair_at(const uint32_t* bits, int64_t f) {
+  const u32x2_dw v = *reinterpret_cast<const u32x2_dw*>(bits + (f >> 5));
+  return u32x2{v[0], v[1]};
+}
+__device__ __forceinline__ uint32_t mask_bits_of(u32x2 pair, int shift) {
+  return (uint32_t)((((uint64_t)pair[1] << 32) | pair[0]) >> shift);
 }
 
 // General custom mask: token j0 + 16 st + 4 g4 + e of a lane's query row is visible iff
@@ -611,6 +616,16 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       l_run[nt] = 0.f;
     }
 
+    // CUSTOM: the mask words of the next tile to run, loaded one tile ahead (with the K
+    // prefetch) and shifted into place only when the tile runs, so that a tile's masking
+    // waits for nothing the tile does not wait for already (loads complete in order: a
+    // use right after the load would wait for the K prefetch issued before it).  A
+    // segment's first tile loads its own.  Tiles start at multiples of 32 tokens, so the
+    // shift is the row's bit offset mod 32 for every tile.
+    u32x2 tw_next[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) tw_next[nt] = u32x2{0u, 0u};
+
     // Prefetch target after the last tile of this segment: the first tile of the next
     // segment, or (at the end of the schedule) the last tile again.
     const int end_tile = has_next ? nxt.t0 : max(cur.t1 - 1, 0);
@@ -621,9 +636,10 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
     // loads issued as soon as their registers are free.  MASKED is a compile-time
     // flag: the body loop over tiles that need no per-element mask is branch-free
     // around its loads, which keeps the compiler's load-wait counting exact.
-    auto tile_step = [&](int tile, auto masked_tag, auto prefetch_tag) {
+    auto tile_step = [&](int tile, auto masked_tag, auto prefetch_tag, auto first_tag) {
       constexpr bool MASKED = decltype(masked_tag)::value;
       constexpr bool PREFETCH = decltype(prefetch_tag)::value;
+      constexpr bool FIRST = decltype(first_tag)::value;  // CUSTOM: no bits loaded ahead
       const int j0 = tile * kTile;
       const bool last = tile + 1 >= cur.t1;
       const int pf_tile = last ? end_tile : tile + 1;
@@ -634,11 +650,15 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       // letting them be hoisted into registers the pipelined tiles need.
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      // (CUSTOM: every tile is masked; its mask bits load with the tile's scores)
+      // (CUSTOM: the tile's mask bits, loaded during the previous tile)
       uint32_t tw[NT];
       if constexpr (CUSTOM) {
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) tw[nt] = mask_bits_at(p.mask_words + p.bits_base, mrow[nt] + j0);
+        for (int nt = 0; nt < NT; ++nt) {
+          const u32x2 pair =
+              FIRST ? mask_pair_at(p.mask_words + p.bits_base, mrow[nt] + j0) : tw_next[nt];
+          tw[nt] = mask_bits_of(pair, (int)(mrow[nt] & 31));
+        }
       }
 
       f32x4 sacc[2][NT];
@@ -658,16 +678,35 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       // at the loop back-edge that waits for the load to complete).
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (PREFETCH) load_tile_k(pf_tile, pf_kv, pf_pages);
+      if constexpr (CUSTOM && PREFETCH) {
+        // the next tile of this segment (its last tile again at the segment's end: the
+        // next segment loads its own first bits)
+        const int64_t jn = (int64_t)min(tile + 1, cur.t1 - 1) * kTile;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          tw_next[nt] = mask_pair_at(p.mask_words + p.bits_base, mrow[nt] + jn);
+      }
 
-      if constexpr (CUSTOM)
-        mask_tile_bits<NT>(sacc, rm, tw, j0, g4);
-      else if constexpr (MASKED)
+      // CUSTOM: a tile inside the kv range whose 32 bits are set in every row of the wave
+      // needs no mask and no zeroed V rows (uniform branches around register work only).
+      const bool past_end = j0 + kTile > cur.kv_len;
+      if constexpr (CUSTOM) {
+        bool partial = past_end;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) partial |= tw[nt] != ~0u;
+        if (__builtin_amdgcn_ballot_w64(partial) != 0) mask_tile_bits<NT>(sacc, rm, tw, j0, g4);
+      } else if constexpr (MASKED) {
         mask_tile<NT>(sacc, rm, j0, g4, diag, sink_end, win_beg);
+      }
 
       uint32_t pb[NT][4];
       softmax_tile<DT, NJ, NT>(sacc, p.scale_log2, m_ref, l_run, o, pb);
 
-      if constexpr (MASKED || CUSTOM) zero_rows_past_end<VW>(vraw, j0, g4, cur.kv_len);
+      if constexpr (CUSTOM) {
+        if (past_end) zero_rows_past_end<VW>(vraw, j0, g4, cur.kv_len);
+      } else if constexpr (MASKED) {
+        zero_rows_past_end<VW>(vraw, j0, g4, cur.kv_len);
+      }
       u32x4 va[NJ];
       transpose_v<NJ, VW>(vraw, va);
       // The transposed operands must be complete before the V registers are refilled:
@@ -689,11 +728,23 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
       // after the loops (masked form, valid for any tile).
       const int t_end = has_next ? cur.t1 : cur.t1 - 1;
       const int t_split = max(cur.t0, min(t_end, limit / kTile));
-      for (int tile = cur.t0; tile < t_split; ++tile)
-        tile_step(tile, std::false_type(), std::true_type());
-      for (int tile = t_split; tile < t_end; ++tile)
-        tile_step(tile, std::true_type(), std::true_type());
-      if (!has_next) tile_step(cur.t1 - 1, std::true_type(), std::false_type());
+      const std::true_type yes;
+      const std::false_type no;
+      if constexpr (CUSTOM) {
+        // the segment's first tile loads its own mask bits; every later tile's come
+        // from the step before it (the same load order on every path into the loop)
+        if (t_end > cur.t0) {
+          tile_step(cur.t0, yes, yes, yes);
+          for (int tile = cur.t0 + 1; tile < t_end; ++tile) tile_step(tile, yes, yes, no);
+          if (!has_next) tile_step(cur.t1 - 1, yes, no, no);
+        } else {
+          tile_step(cur.t1 - 1, yes, no, yes);  // the schedule's last tile, alone
+        }
+      } else {
+        for (int tile = cur.t0; tile < t_split; ++tile) tile_step(tile, no, yes, no);
+        for (int tile = t_split; tile < t_end; ++tile) tile_step(tile, yes, yes, no);
+        if (!has_next) tile_step(cur.t1 - 1, yes, no, no);
+      }
     } else if (has_next) {
       // No tile ran, so the prefetched tile was not consumed: load the next
       // segment's first tile now.
