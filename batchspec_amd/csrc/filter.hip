@@ -1083,8 +1083,8 @@ struct SplitArgs {
   float top_p;
   RowInfo* info;
   int32_t* lists;    // [rows][kCap]
-  float* lane_s;     // [rows][kLanes]
-  float* lane_r;     // [rows][kLanes]
+  float* lane_s;     // [rows][8][kThreads]: lane 8 t + i at [i][t]
+  float* lane_r;     // [rows][8][kThreads]
   PartOut* parts;    // [rows][kParts]
   uint32_t* ckeys;   // [rows][kParts][kPartList]
   int32_t* cidx;     // [rows][kParts][kPartList]
@@ -1152,9 +1152,11 @@ __device__ __forceinline__ uint32_t fine_bound_inline(RowsLds& L, const uint32_t
   return bin < 0 ? 0u : (top - (uint32_t)bin) << 16;
 }
 
-template <int N>
-__device__ __noinline__ uint32_t fine_bound(RowsLds& L, const uint32_t (&key)[N], int k) {
-  return fine_bound_inline<N>(L, key, k);
+// Out-of-line form of four keys per thread.  The keys travel by value, in registers: an
+// array passed by reference to a call would be stored to scratch memory and read back.
+__device__ __noinline__ uint32_t fine_bound4(RowsLds& L, u32x4 key4, int k) {
+  const uint32_t key[4] = {key4[0], key4[1], key4[2], key4[3]};
+  return fine_bound_inline<4>(L, key, k);
 }
 
 template <int DT>
@@ -1388,12 +1390,13 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
     do_round(cq, w[0], gm, x);
   }
   // lane states and the part's maximum
+  // lane 8 ct + i at [i][ct]: a wave's stores of one i cover 64 consecutive floats
   float* ls = a.lane_s + r * kLanes;
   float* lr = a.lane_r + r * kLanes;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    ls[8 * ct + i0 + e] = st[e].s;
-    lr[8 * ct + i0 + e] = st[e].r;
+    ls[(i0 + e) * kThreads + ct] = st[e].s;
+    lr[(i0 + e) * kThreads + ct] = st[e].r;
   }
   float mx = fmaxf(st[0].m, st[1].m);
 #pragma unroll
@@ -1455,10 +1458,11 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
       ci[j] = s < n ? L.cidx[s] : 0;
       if (s < n) cv[j] = key_value(ck[j]);
     }
+    static_assert(PER == 4, "fine_bound4 takes four keys per thread");
     uint32_t lk[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) lk[j] = t + kThreads * j < n ? ck[j] : 0u;
-    uint32_t kb = fine_bound<PER>(L, lk, k);
+    uint32_t kb = fine_bound4(L, u32x4{lk[0], lk[1], lk[2], lk[3]}, k);
     if (kb == 0u)
       kb = kth_key_call(L, cv[0], cv[1], cv[2], cv[3], cv[4], cv[5], cv[6], cv[7], k);
     if (t == 0) L.nk = 0;
@@ -1516,11 +1520,15 @@ __global__ void __launch_bounds__(kThreads) filter_combine_kernel(SplitArgs a) {
 #pragma unroll
   for (int q = 1; q < kParts; ++q) mx = fmaxf(mx, po[q].m);
   const float rho_m = mx * c;
-  const f32x4* ls4 = reinterpret_cast<const f32x4*>(a.lane_s + r * kLanes + 8 * t);
-  const f32x4* lr4 = reinterpret_cast<const f32x4*>(a.lane_r + r * kLanes + 8 * t);
-  const f32x4 s0 = ls4[0], s1 = ls4[1], r0 = lr4[0], r1 = lr4[1];
-  const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-  const float rv[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+  // lane 8 t + i of the row at [i][t] (the parts' layout)
+  const float* lsr = a.lane_s + r * kLanes + t;
+  const float* lrr = a.lane_r + r * kLanes + t;
+  float sv[8], rv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    sv[i] = lsr[i * kThreads];
+    rv[i] = lrr[i * kThreads];
+  }
   float rs[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) rs[i] = canon::lane_rescaled(LaneState{-INFINITY, sv[i], rv[i]}, rho_m);
