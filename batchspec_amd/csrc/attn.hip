@@ -782,12 +782,15 @@ struct SharedTile {
   static constexpr int kHalfBytes = kTile * D * 2;  // K (or V) part of one head's tile
   static constexpr int kHeadBytes = 2 * kHalfBytes;
   static constexpr int kChunks = kHeadBytes / 1024;  // 1 KB direct loads per head tile
-  // Column swizzle (XOR of the 16-byte column with a linear function of the token):
-  // the 8 or 16 lanes served together by the LDS fall into distinct 16-byte bank
-  // groups, both for the K reads (one column of 16 consecutive tokens) and for the
-  // transposing V reads (two columns of 4 consecutive tokens per 16 lanes).
+  // Column swizzle (XOR of the 16-byte column with a function of the token), chosen so
+  // that both operand reads run without LDS bank conflicts: the K reads (16-byte reads,
+  // one column of 16 consecutive tokens per 16 lanes) and the transposing V reads
+  // (8-byte reads, two columns of 4 consecutive tokens per 16 lanes).  For D = 128,
+  // measured with the LDS conflict counter on gfx950: t ^ 12 (t & 1) gives both reads
+  // their conflict-free time (4 and 2 cycles per instruction); t ^ 8 (t & 1) doubled the
+  // K reads' (a 2-way conflict), and t alone doubled the V reads'.
   __device__ static __forceinline__ int swz(int t) {
-    if constexpr (D == 128) return (t & 15) ^ ((t & 1) << 3);
+    if constexpr (D == 128) return (t & 15) ^ ((t & 1) * 12);
     return ((t >> 1) & 3) | (((t ^ (t >> 1) ^ (t >> 3)) & 1) << 2);
   }
   // granule index of (token t, column c) inside a K or V half
