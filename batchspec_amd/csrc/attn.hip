@@ -788,10 +788,11 @@ struct SharedTile {
   // (8-byte reads, two columns of 4 consecutive tokens per 16 lanes).  For D = 128,
   // measured with the LDS conflict counter on gfx950: t ^ 12 (t & 1) gives both reads
   // their conflict-free time (4 and 2 cycles per instruction); t ^ 8 (t & 1) doubled the
-  // K reads' (a 2-way conflict), and t alone doubled the V reads'.
+  // K reads' (a 2-way conflict), and t alone doubled the V reads'.  For D = 64 (8
+  // columns), t mod 8 gives both their conflict-free time.
   __device__ static __forceinline__ int swz(int t) {
     if constexpr (D == 128) return (t & 15) ^ ((t & 1) * 12);
-    return ((t >> 1) & 3) | (((t ^ (t >> 1) ^ (t >> 3)) & 1) << 2);
+    return t & 7;
   }
   // granule index of (token t, column c) inside a K or V half
   __device__ static __forceinline__ int at(int t, int c) {
