@@ -501,27 +501,55 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
   auto page_pos = [&](int jsc, int kv_len, int page_start) -> int {
     return kv_len > 0 ? page_start + (jsc >> p.page_shift) : p.safe_pos;
   };
+  // K loads cover whole 128-byte lines: load j of a subtile reads, in lane (c16, g4),
+  // token (c16 & 7) + 8 (j & 1), bytes 128 (j >> 1) + 16 (g4 + 4 (c16 >> 3)) of the head's
+  // slice, so one load is 8 token rows x 128 bytes.  (The A-operand layout, 16 token rows
+  // x 64 bytes per load, requested every line twice, in two half-line requests, which
+  // doubles the memory requests per byte of K.)  kfix() moves the data into the A layout.
+  const int ktok = c16 & 7;
+  const uint32_t kbyte = (uint32_t)(16 * (g4 + 4 * (c16 >> 3)));
   auto load_tile_k = [&](int tile, int kv_len, int page_start) {
     const int j0 = tile * kTile;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const int js = j0 + 16 * st;
-      const char* base;
-      uint32_t off;
-      if constexpr (PS_GE16) {
-        const int jsc = js < kv_len ? js : 0;  // subtile start, clamped into the request
-        const int page = ld_uniform(p.kv_indices, page_pos(jsc, kv_len, page_start));
-        base = p.k_cache + (int64_t)page * p.page_stride_bytes;
-        off = (uint32_t)(((jsc & p.page_mask) + c16) * tok_bytes) + head_off;
-      } else {
-        const int j = max(min(js + c16, kv_len - 1), 0);
-        const int page = p.kv_indices[page_pos(j, kv_len, page_start)];
-        base = p.k_cache + (int64_t)page * p.page_stride_bytes;
-        off = (uint32_t)((j & p.page_mask) * tok_bytes) + head_off;
-      }
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kreg[st][s] = ld_stream(base + off + (32 * s + 8 * g4) * 2);
+      for (int h = 0; h < 2; ++h) {  // token rows ktok + 8 h
+        const char* base;
+        uint32_t off;
+        if constexpr (PS_GE16) {
+          const int jsc = js < kv_len ? js : 0;  // subtile start, clamped into the request
+          const int page = ld_uniform(p.kv_indices, page_pos(jsc, kv_len, page_start));
+          base = p.k_cache + (int64_t)page * p.page_stride_bytes;
+          off = (uint32_t)(((jsc & p.page_mask) + ktok + 8 * h) * tok_bytes) + head_off + kbyte;
+        } else {
+          const int j = max(min(js + ktok + 8 * h, kv_len - 1), 0);
+          const int page = p.kv_indices[page_pos(j, kv_len, page_start)];
+          base = p.k_cache + (int64_t)page * p.page_stride_bytes;
+          off = (uint32_t)((j & p.page_mask) * tok_bytes) + head_off + kbyte;
+        }
+#pragma unroll
+        for (int q = 0; q < KS / 2; ++q) kreg[st][2 * q + h] = ld_stream(base + off + 128 * q);
+      }
     }
+  };
+  // The A operand of k-step s (token c16, bytes 64 s + 16 g4): for s = 2q, lanes c16 < 8
+  // hold it already in load 2q, the others find it in load 2q+1 eight lanes away; for
+  // s = 2q+1 the other way round.  Eight lanes away = a row rotation by 8 (DPP).
+  const bool klow = c16 < 8;
+  auto kfix = [&](const u32x4 (&x)[2][KS], u32x4 (&a)[2][KS]) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int q = 0; q < KS / 2; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t x0 = x[st][2 * q][e], x1 = x[st][2 * q + 1][e];
+          const uint32_t r0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)x0, 0x128, 0xf, 0xf, false);
+          const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)x1, 0x128, 0xf, 0xf, false);
+          a[st][2 * q][e] = klow ? x0 : r1;
+          a[st][2 * q + 1][e] = klow ? r0 : x1;
+        }
   };
   auto load_tile_v = [&](int tile, int kv_len, int page_start) {
     const int j0 = tile * kTile;
@@ -661,6 +689,8 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
         }
       }
 
+      u32x4 kop[2][KS];
+      kfix(kreg, kop);
       f32x4 sacc[2][NT];
 #pragma unroll
       for (int st = 0; st < 2; ++st)
@@ -669,7 +699,7 @@ __global__ void __launch_bounds__(512) verify_attn_kernel(Params p) {
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int s = 0; s < KS; ++s)
-            acc = mfma16x16x32<DT>(kreg[st][s], q_lds[wave][nt * KS + s][lane], acc);
+            acc = mfma16x16x32<DT>(kop[st][s], q_lds[wave][nt * KS + s][lane], acc);
           sacc[st][nt] = acc;
         }
       // K registers are free: prefetch.  The scheduling barriers keep each prefetch
