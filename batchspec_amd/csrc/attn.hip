@@ -11,7 +11,8 @@
 //   * kv tokens are consumed in tiles of 32 (two 16-token subtiles); a subtile of a
 //     page_size >= 16 cache lies inside one page, so its page id is wave-uniform;
 //   * scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32 (A = K
-//     rows straight from the cache, B = Q^T from LDS).  In the accumulator layout
+//     rows from the cache, loaded as whole 128-byte lines and rotated into the A
+//     layout in registers; B = Q^T from LDS).  In the accumulator layout
 //     each lane then holds one query row, so the softmax statistics are lane-local
 //     up to a 4-lane reduction;
 //   * the output is accumulated transposed as well, O^T = V^T P^T.  P^T is already in
