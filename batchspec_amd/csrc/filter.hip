@@ -1489,12 +1489,12 @@ __global__ void __launch_bounds__(kThreads) filter_parts_kernel(SplitArgs a) {
   if (t == 0) a.parts[r * kParts + p] = po;
 }
 
+// The combine of row r by the whole workgroup (filter_combine_kernel, and the fallback of
+// filter_request_kernel).
 template <int DT>
-__global__ void __launch_bounds__(kThreads) filter_combine_kernel(SplitArgs a) {
-  __shared__ __align__(16) RowsLds L;
-  __shared__ float wave_val[kThreads / 64];
+__device__ __forceinline__ void combine_row(const SplitArgs& a, int64_t r, RowsLds& L,
+                                            float (&wave_val)[kThreads / 64]) {
   const int t = threadIdx.x;
-  const int64_t r = blockIdx.x;
   const int64_t V = a.V;
   const char* row = split_row<DT>(a, r);
   const float c = a.c;
@@ -1578,6 +1578,13 @@ __global__ void __launch_bounds__(kThreads) filter_combine_kernel(SplitArgs a) {
     large_threshold<DT>(L, row, V, vec, c, neg, use_k, use_p, a.top_k, target);
   }
   write_info(L, a.info + r, M);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) filter_combine_kernel(SplitArgs a) {
+  __shared__ __align__(16) RowsLds L;
+  __shared__ float wave_val[kThreads / 64];
+  combine_row<DT>(a, blockIdx.x, L, wave_val);
 }
 
 // ----------------------------------------------------------------------------
@@ -1809,17 +1816,31 @@ __global__ void __launch_bounds__(kThreads) filter_tiles_kernel(ChainArgs a) {
   }
 }
 
+// LDS of the chain of one request.
+struct ChainLds {
+  int s_j, s_n, s_tok, s_last, s_tile, s_last_tile;
+  int32_t lv[kCap];
+  uint64_t lr[kCap];
+  uint64_t s_acc, s_tbase;
+  uint64_t excl[kThreads];
+  uint64_t s_wave[kThreads / 64];
+  uint64_t tsum[kMaxTiles];
+  uint64_t tloc[2][kMaxTiles];  // tile sums made here (tiles_ready == 0)
+};
+
+// The chain of request b by the whole workgroup, from the row infos and lists in the
+// workspace (filter_chain_kernel, and the fallback of filter_request_kernel).
 template <int DT>
-__global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
-  __shared__ int s_j, s_n, s_tok, s_last, s_tile, s_last_tile;
-  __shared__ int32_t lv[kCap];
-  __shared__ uint64_t lr[kCap];
-  __shared__ uint64_t s_acc, s_tbase;
-  __shared__ uint64_t excl[kThreads];
-  __shared__ uint64_t s_wave[kThreads / 64];
-  __shared__ uint64_t tsum[kMaxTiles];
-  __shared__ uint64_t tloc[2][kMaxTiles];  // tile sums made here (tiles_ready == 0)
-  const int b = blockIdx.x;
+__device__ __forceinline__ void chain_request(const ChainArgs& a, int b, ChainLds& S) {
+  int &s_j = S.s_j, &s_n = S.s_n, &s_tok = S.s_tok, &s_last = S.s_last, &s_tile = S.s_tile,
+      &s_last_tile = S.s_last_tile;
+  int32_t(&lv)[kCap] = S.lv;
+  uint64_t(&lr)[kCap] = S.lr;
+  uint64_t &s_acc = S.s_acc, &s_tbase = S.s_tbase;
+  uint64_t(&excl)[kThreads] = S.excl;
+  uint64_t(&s_wave)[kThreads / 64] = S.s_wave;
+  uint64_t(&tsum)[kMaxTiles] = S.tsum;
+  uint64_t(&tloc)[2][kMaxTiles] = S.tloc;
   const int t = threadIdx.x;
   const int k = a.k;
   const int64_t V = a.V;
@@ -2001,6 +2022,527 @@ __global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
   }
 }
 
+template <int DT>
+__global__ void __launch_bounds__(kThreads) filter_chain_kernel(ChainArgs a) {
+  __shared__ ChainLds S;
+  chain_request<DT>(a, blockIdx.x, S);
+}
+
+// ---- The split path's tail in one launch per request --------------------------------
+//
+// filter_request_kernel (grid B, four waves) replaces filter_combine_kernel +
+// filter_chain_kernel for requests of at most kFastRows rows with one-hot drafts.  It
+// keeps filter_combine_kernel's arithmetic and order:
+//   - (M, Z): wave w evaluates slice w of every row's canonical tree (canonical threads
+//     64 w .. 64 w + 63: the same eight-term sums and the same butterfly within the
+//     slice), and Z is the same sum of the four slice sums;
+//   - the walk of row i (wave i mod 4) over the parts' keys at or above the largest part
+//     bound: t* is the largest key whose count (keys at or above it) reaches top_k or
+//     whose mass reaches the target.  Counts and masses are integers, so any evaluation
+//     order gives the same t* and Z_K.  Here the top_k-th largest key T is selected first
+//     (a bitwise search over ballots), and only the keys at or above T get their count
+//     and mass: T itself reaches by count, so t* >= T.  With fewer than top_k keys, T is
+//     0 and every key is examined, as in the workgroup walk.
+// It covers the rows whose parts each listed at most kFastPart keys and whose walk finds
+// t* among them.  A request with any other row runs combine_row on those rows and
+// chain_request (the whole workgroup, through the workspace), which give the same bits.
+// The chain then runs on the first wave from the rows' infos and kept keys in LDS; an
+// element's weight is a function of its key (key_value(okey(x)) is x, or +0 for -0,
+// whose weight is the same).
+constexpr int kFastRows = 8;                    // rows of a request (k + 1)
+constexpr int kFastPart = 32;                   // keys of a part read by the walk
+constexpr int kFastCands = kParts * kFastPart;  // candidate slots of a row: two per lane
+constexpr int kFastTopK = kFastPart - 8;        // largest top_k sent to filter_request_kernel
+static_assert(kFastCands == 128 && kFastPart <= kPartList, "two candidate slots per lane");
+
+struct FastLds {
+  uint32_t key[kFastRows][kFastCands];  // the kept keys of the row (keys >= t*)
+  int32_t idx[kFastRows][kFastCands];   // and their indices
+  uint32_t tkey[kFastRows][kFastCands]; // the walk's keys >= T, pads of key 0 to x4
+  uint64_t tm[kFastRows][kFastCands];   // their masses (the chain's row: draw weights)
+  RowInfo info[kFastRows];
+  int ok[kFastRows];                    // the wave walk finished the row
+  float zs[kFastRows][kThreads / 64];   // slice sums of the canonical trees
+  int64_t xid[kFastRows];               // draft token of position i
+  float xval[kFastRows];                // the target logit of row i at it (when in range)
+};
+
+// Set bits of m in the lanes below this one.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Wave reductions on the DPP network (no LDS round trips): quad permutations [1,0,3,2]
+// and [2,3,0,1] (partners l ^ 1, l ^ 2), then the mirrors within 8 and 16 lanes, which
+// reach the other half of the 8 / 16 lanes once each half holds one value, then the four
+// rows of 16 read as scalars.  For the float sum this is the butterfly
+// s = s + shfl_xor(s, m), m = 1 .. 32, bit for bit: each step adds the same two values
+// as the butterfly (in either order, which addition does not see), and the last two
+// steps are (R0 + R1) + (R2 + R3) over the row sums.  Every lane must be active.
+constexpr int kDppXor1 = 0xb1, kDppXor2 = 0x4e, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  return ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
+}
+
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int l) {
+  return ((uint64_t)lane_u32((uint32_t)(v >> 32), l) << 32) | lane_u32((uint32_t)v, l);
+}
+
+__device__ __forceinline__ float wave_tree_sum(float s) {
+  s = s + __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(s)));
+  s = s + __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(s)));
+  s = s + __uint_as_float(dpp_u32<kDppHalfMirror>(__float_as_uint(s)));
+  s = s + __uint_as_float(dpp_u32<kDppMirror>(__float_as_uint(s)));
+  const float r0 = __uint_as_float(lane_u32(__float_as_uint(s), 0));
+  const float r1 = __uint_as_float(lane_u32(__float_as_uint(s), 16));
+  const float r2 = __uint_as_float(lane_u32(__float_as_uint(s), 32));
+  const float r3 = __uint_as_float(lane_u32(__float_as_uint(s), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<kDppXor1>(v));
+  v = max(v, dpp_u32<kDppXor2>(v));
+  v = max(v, dpp_u32<kDppHalfMirror>(v));
+  v = max(v, dpp_u32<kDppMirror>(v));
+  return max(max(lane_u32(v, 0), lane_u32(v, 16)), max(lane_u32(v, 32), lane_u32(v, 48)));
+}
+
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+  v |= dpp_u32<kDppXor1>(v);
+  v |= dpp_u32<kDppXor2>(v);
+  v |= dpp_u32<kDppHalfMirror>(v);
+  v |= dpp_u32<kDppMirror>(v);
+  return (lane_u32(v, 0) | lane_u32(v, 16)) | (lane_u32(v, 32) | lane_u32(v, 48));
+}
+
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+  v = min(v, dpp_u64<kDppXor1>(v));
+  v = min(v, dpp_u64<kDppXor2>(v));
+  v = min(v, dpp_u64<kDppHalfMirror>(v));
+  v = min(v, dpp_u64<kDppMirror>(v));
+  return min(min(lane_u64(v, 0), lane_u64(v, 16)), min(lane_u64(v, 32), lane_u64(v, 48)));
+}
+
+__device__ __forceinline__ uint64_t wave_add_u64(uint64_t v) {
+  v += dpp_u64<kDppXor1>(v);
+  v += dpp_u64<kDppXor2>(v);
+  v += dpp_u64<kDppHalfMirror>(v);
+  v += dpp_u64<kDppMirror>(v);
+  return (lane_u64(v, 0) + lane_u64(v, 16)) + (lane_u64(v, 32) + lane_u64(v, 48));
+}
+
+__device__ __forceinline__ int wave_min_i32(int v) {
+  v = min(v, (int)dpp_u32<kDppXor1>((uint32_t)v));
+  v = min(v, (int)dpp_u32<kDppXor2>((uint32_t)v));
+  v = min(v, (int)dpp_u32<kDppHalfMirror>((uint32_t)v));
+  v = min(v, (int)dpp_u32<kDppMirror>((uint32_t)v));
+  return min(min((int)lane_u32(v, 0), (int)lane_u32(v, 16)),
+             min((int)lane_u32(v, 32), (int)lane_u32(v, 48)));
+}
+
+__device__ __forceinline__ int wave_max_i32(int v) {
+  v = max(v, (int)dpp_u32<kDppXor1>((uint32_t)v));
+  v = max(v, (int)dpp_u32<kDppXor2>((uint32_t)v));
+  v = max(v, (int)dpp_u32<kDppHalfMirror>((uint32_t)v));
+  v = max(v, (int)dpp_u32<kDppMirror>((uint32_t)v));
+  return max(max((int)lane_u32(v, 0), (int)lane_u32(v, 16)),
+             max((int)lane_u32(v, 32), (int)lane_u32(v, 48)));
+}
+
+// What the walk of a row reads: the part records and the first kFastPart key slots of
+// each part (slot s = lane + 64 h of the lane: part s / kFastPart).
+struct WalkIn {
+  PartOut po[kParts];
+  uint32_t sk[2];
+  int32_t si[2];
+};
+
+__device__ __forceinline__ void walk_load(const SplitArgs& a, int64_t r, WalkIn& in) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int q = 0; q < kParts; ++q) in.po[q] = a.parts[r * kParts + q];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int s = lane + 64 * h;
+    const int64_t at = (r * kParts + s / kFastPart) * kPartList + s % kFastPart;
+    in.sk[h] = a.ckeys[at];
+    in.si[h] = a.cidx[at];
+  }
+}
+
+// Loaded values in registers here: a wave's loads are in flight together before the
+// first wait (the compiler would otherwise move loads into the branches that use them).
+__device__ __forceinline__ void walk_pin(const WalkIn& in) {
+#pragma unroll
+  for (int q = 0; q < kParts; ++q)
+    asm volatile("" ::"v"(in.po[q].m), "v"(in.po[q].kb), "v"(in.po[q].count));
+  asm volatile("" ::"v"(in.sk[0]), "v"(in.sk[1]), "v"(in.si[0]), "v"(in.si[1]));
+}
+
+// The top_k-th largest of the keys held (kj[h] where val[h]), or 0 when fewer than top_k
+// are held: the largest T with at least top_k keys >= T, built bit by bit from the top.
+// Every held key has the largest key's bits outside `diff` (the bits where some key
+// differs from it), so T starts from those and only the bits of diff are decided.
+__device__ __forceinline__ uint32_t kth_largest_held(const uint32_t (&kj)[2], const bool (&val)[2],
+                                                     int top_k) {
+  const int held = __builtin_popcountll(__builtin_amdgcn_ballot_w64(val[0])) +
+                   __builtin_popcountll(__builtin_amdgcn_ballot_w64(val[1]));
+  if (held < top_k) return 0u;
+  const uint32_t hi = wave_max_u32(max(val[0] ? kj[0] : 0u, val[1] ? kj[1] : 0u));
+  uint32_t diff = wave_or_u32((val[0] ? kj[0] ^ hi : 0u) | (val[1] ? kj[1] ^ hi : 0u));
+  uint32_t T = hi & ~diff;
+  while (diff != 0u) {
+    const uint32_t bit = 1u << (31 - __builtin_clz(diff));
+    diff &= ~bit;
+    const uint32_t cand = T | bit;
+    const int c = __builtin_popcountll(__builtin_amdgcn_ballot_w64(val[0] && kj[0] >= cand)) +
+                  __builtin_popcountll(__builtin_amdgcn_ballot_w64(val[1] && kj[1] >= cand));
+    if (c >= top_k) T = cand;
+  }
+  return T;
+}
+
+// The walk of row r by one wave, with its statistics (M, Z): its info and kept list into
+// the workspace and F (slot `slot`).  Returns false (in every lane, writing no info)
+// when the row needs the workgroup's combine.
+__device__ __forceinline__ bool fast_walk(const SplitArgs& a, int64_t r, int slot,
+                                          const WalkIn& in, float M, float Z, FastLds& F) {
+  const int lane = threadIdx.x & 63;
+  const float c = a.c;
+  const bool use_k = a.top_k > 0 && (int64_t)a.top_k < a.V;
+  const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
+  if (!use_k) return false;
+  bool can = true;
+  uint32_t bkey = 0u;
+#pragma unroll
+  for (int q = 0; q < kParts; ++q) {
+    can = can && in.po[q].count >= 0 && in.po[q].count <= kFastPart;
+    bkey = max(bkey, in.po[q].kb);
+  }
+  if (!can) return false;
+  const float neg = -(M * c);
+  const uint64_t target = use_p ? (uint64_t)ceilf((a.top_p * Z) * 0x1p40f) : 0ull;
+  // the written keys at or above B = max kb_p: every element of the row there
+  bool val[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int s = lane + 64 * h;
+    const int q = s / kFastPart;
+    int cnt = in.po[0].count;
+#pragma unroll
+    for (int qq = 1; qq < kParts; ++qq) cnt = q == qq ? in.po[qq].count : cnt;
+    val[h] = s % kFastPart < cnt && in.sk[h] >= bkey;
+  }
+  const uint32_t T = kth_largest_held(in.sk, val, a.top_k);
+  // count and mass of each key >= T over the keys >= T (every key at or above one of
+  // them is one of them); the keys in turn, from the ballot of each slot
+  bool top[2];
+  uint64_t cm[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    top[h] = val[h] && in.sk[h] >= T;
+    cm[h] = top[h] ? fx40(canon::weight(key_value(in.sk[h]), c, neg)) : 0ull;
+  }
+  // the keys >= T and their masses into LDS (slot order, pads of key 0 and mass 0 to a
+  // multiple of 4), then each key's count and mass over them, four per read
+  typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+  const uint64_t t0 = __builtin_amdgcn_ballot_w64(top[0]);
+  const uint64_t t1 = __builtin_amdgcn_ballot_w64(top[1]);
+  const int m0 = __builtin_popcountll(t0);
+  const int m = m0 + __builtin_popcountll(t1);
+  const int m4 = (m + 3) & ~3;
+  uint32_t* tkey = F.tkey[slot];
+  uint64_t* tm = F.tm[slot];
+  if (top[0]) {
+    tkey[lanes_below(t0)] = in.sk[0];
+    tm[lanes_below(t0)] = cm[0];
+  }
+  if (top[1]) {
+    tkey[m0 + lanes_below(t1)] = in.sk[1];
+    tm[m0 + lanes_below(t1)] = cm[1];
+  }
+  if (lane < m4 - m) {
+    tkey[m + lane] = 0u;
+    tm[m + lane] = 0ull;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  uint32_t cnt[2] = {0u, 0u};
+  uint64_t ms[2] = {0ull, 0ull};
+  for (int q = 0; q < m4; q += 4) {
+    const u32x4 kk = *reinterpret_cast<const u32x4*>(tkey + q);
+    const u64x2 ma = *reinterpret_cast<const u64x2*>(tm + q);
+    const u64x2 mb = *reinterpret_cast<const u64x2*>(tm + q + 2);
+    const uint64_t mm[4] = {ma[0], ma[1], mb[0], mb[1]};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bool ge = kk[e] >= in.sk[h];
+        cnt[h] += ge ? 1u : 0u;
+        ms[h] += ge ? mm[e] : 0ull;
+      }
+  }
+  // t* = the largest key that reaches; Z_K = its mass, which is the smallest mass of the
+  // keys that reach (mass does not increase with the key; equal keys hold equal masses)
+  uint32_t best = 0u;
+  uint64_t least = ~0ull;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    if (top[h] && reached(use_k, use_p, cnt[h], ms[h], a.top_k, target)) {
+      best = max(best, in.sk[h]);
+      least = min(least, ms[h]);
+    }
+  const uint32_t tk = wave_max_u32(best);
+  const uint64_t zk = wave_min_u64(least);
+  if (tk == 0u) return false;
+  // the kept keys (>= t*) with their indices, in slot order
+  const bool k0 = val[0] && in.sk[0] >= tk;
+  const bool k1 = val[1] && in.sk[1] >= tk;
+  const uint64_t l0 = __builtin_amdgcn_ballot_w64(k0);
+  const uint64_t l1 = __builtin_amdgcn_ballot_w64(k1);
+  const int nl0 = __builtin_popcountll(l0);
+  int32_t* lo = a.lists + r * kCap;
+  if (k0) {
+    const int p = lanes_below(l0);
+    lo[p] = in.si[0];
+    F.key[slot][p] = in.sk[0];
+    F.idx[slot][p] = in.si[0];
+  }
+  if (k1) {
+    const int p = nl0 + lanes_below(l1);
+    lo[p] = in.si[1];
+    F.key[slot][p] = in.sk[1];
+    F.idx[slot][p] = in.si[1];
+  }
+  RowInfo ri;
+  ri.m = M;
+  ri.inv_k = 1.0f / (canon::u64_to_f32(zk) * 0x1p-40f);
+  ri.t_key = tk;
+  ri.n_list = nl0 + __builtin_popcountll(l1);
+  if (lane == 0) {
+    a.info[r] = ri;
+    F.info[slot] = ri;
+  }
+  return true;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) filter_request_kernel(SplitArgs sa, ChainArgs ca) {
+  __shared__ __align__(16) FastLds F;
+  __shared__ __align__(16) RowsLds L;
+  __shared__ float wave_val[kThreads / 64];
+  __shared__ ChainLds S;
+  const int b = blockIdx.x;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int k = ca.k;
+  const int nrows = k + 1;
+  const int64_t V = ca.V;
+  const int64_t trow0 = (int64_t)b * nrows;
+  const float c = ca.c;
+  static_assert(kFastRows == 2 * (kThreads / 64), "two walk rows per wave at most");
+  const int i0 = wave, i1 = wave + kThreads / 64;  // the wave's walk rows
+
+  // Every load first: the draft tokens (the last wave), the lane states of slice `wave`
+  // and the part maxima of every row, and the walk rows' records and key slots (of the
+  // last row for a wave without a row: loaded, unused).
+  const bool x_lane = wave == kThreads / 64 - 1 && lane < k;
+  const int64_t xid = x_lane ? ca.draft_ids[(int64_t)b * k + lane] : -1;
+  float sv[kFastRows][8], rv[kFastRows][8], pm[kFastRows][kParts];
+  const float* pmf = reinterpret_cast<const float*>(sa.parts);
+  constexpr int kPartFloats = sizeof(PartOut) / 4;
+#pragma unroll
+  for (int i = 0; i < kFastRows; ++i)
+    if (i < nrows) {
+      const int64_t r = trow0 + i;
+      const float* lsr = sa.lane_s + r * kLanes + 64 * wave + lane;
+      const float* lrr = sa.lane_r + r * kLanes + 64 * wave + lane;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sv[i][e] = lsr[e * kThreads];
+        rv[i][e] = lrr[e * kThreads];
+      }
+#pragma unroll
+      for (int q = 0; q < kParts; ++q) pm[i][q] = pmf[(r * kParts + q) * kPartFloats];
+    }
+  WalkIn w0, w1;
+  walk_load(sa, trow0 + min(i0, nrows - 1), w0);
+  walk_load(sa, trow0 + min(i1, nrows - 1), w1);
+#pragma unroll
+  for (int i = 0; i < kFastRows; ++i)
+    if (i < nrows) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) asm volatile("" ::"v"(sv[i][e]), "v"(rv[i][e]));
+#pragma unroll
+      for (int q = 0; q < kParts; ++q) asm volatile("" ::"v"(pm[i][q]));
+    }
+  walk_pin(w0);
+  walk_pin(w1);
+  // the target logit at the draft token (every lane: no branch to wait in; its round
+  // trip overlaps the trees and the walks)
+  const char* xrow = static_cast<const char*>(ca.t_logits) +
+                     (trow0 + (x_lane ? lane : 0)) * V * (DT == BSX_DTYPE_FP32 ? 4 : 2);
+  const bool x_in = xid >= 0 && xid < V;
+  const float xval = load_one<DT>(xrow, x_in ? xid : 0);
+
+  // slice `wave` of every row's canonical tree
+#pragma unroll
+  for (int i = 0; i < kFastRows; ++i)
+    if (i < nrows) {
+      float mx = pm[i][0];
+#pragma unroll
+      for (int q = 1; q < kParts; ++q) mx = fmaxf(mx, pm[i][q]);
+      const float rho_m = mx * c;
+      float rs[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        rs[e] = canon::lane_rescaled(LaneState{-INFINITY, sv[i][e], rv[i][e]}, rho_m);
+      const float zs =
+          wave_tree_sum(((rs[0] + rs[1]) + (rs[2] + rs[3])) + ((rs[4] + rs[5]) + (rs[6] + rs[7])));
+      if (lane == 0) F.zs[i][wave] = zs;
+    }
+  __syncthreads();
+  // the walks
+  auto walk_row = [&](int i, const WalkIn& in) {
+    const float Z = (F.zs[i][0] + F.zs[i][1]) + (F.zs[i][2] + F.zs[i][3]);
+    float M = in.po[0].m;
+#pragma unroll
+    for (int q = 1; q < kParts; ++q) M = fmaxf(M, in.po[q].m);
+    const bool ok = fast_walk(sa, trow0 + i, i, in, M, Z, F);
+    if (lane == 0) F.ok[i] = ok ? 1 : 0;
+  };
+  if (i0 < nrows) walk_row(i0, w0);
+  if (i1 < nrows) walk_row(i1, w1);
+  if (x_lane) {
+    F.xid[lane] = xid;
+    F.xval[lane] = x_in ? xval : 0.0f;
+  }
+  __syncthreads();
+  bool all_ok = true;
+  for (int i = 0; i < nrows; ++i) all_ok = all_ok && F.ok[i] != 0;
+  if (!all_ok) {
+    for (int i = 0; i < nrows; ++i)
+      if (F.ok[i] == 0) {
+        combine_row<DT>(sa, trow0 + i, L, wave_val);
+        __syncthreads();
+      }
+    chain_request<DT>(ca, b, S);
+    return;
+  }
+  if (wave != 0) return;
+
+  // ratio tests (lane i: draft position i), with the one-hot draft q = 1
+  const float* uni = ca.uniforms + trow0;
+  bool acc = false;
+  if (lane < k) {
+    const int64_t x = F.xid[lane];
+    if (x >= 0 && x < V) {
+      const RowInfo ri = F.info[lane];
+      const float xv = F.xval[lane];
+      const float p = okey(xv) >= ri.t_key ? canon::weight(xv, c, -(ri.m * c)) * ri.inv_k : 0.0f;
+      acc = uni[lane] * 1.0f < p;
+    }
+  }
+  const uint64_t acc_bits = __builtin_amdgcn_ballot_w64(acc);
+  const uint64_t rej_bits = __builtin_amdgcn_ballot_w64(lane < k && !acc);
+  const int j = rej_bits != 0ull ? __builtin_ctzll(rej_bits) : k;
+
+  // the draw from row j over its kept keys (entry s in lane s mod 64): r = fx40(max(p' -
+  // q', 0)) against the draft (one at its token) when j < k, else (or when that has no
+  // mass) fx40(p')
+  const RowInfo ri = F.info[j];
+  const int n = ri.n_list;
+  const bool has_q = j < k;
+  const int64_t xj = has_q ? F.xid[j] : -1;
+  const float nmc = -(ri.m * c);
+  bool kept[2];
+  int32_t vid[2];
+  float p[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int s = lane + 64 * h;
+    kept[h] = s < n;
+    vid[h] = kept[h] ? F.idx[j][s] : 0;
+    p[h] = kept[h] ? canon::weight(key_value(F.key[j][s]), c, nmc) * ri.inv_k : 0.0f;
+  }
+  uint64_t w[2] = {0ull, 0ull};
+  uint64_t total = 0ull;
+  for (int pass = 0; pass < 2; ++pass) {
+    const bool with_q = has_q && pass == 0;
+    if (pass == 1 && !has_q) break;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float q = with_q && (int64_t)vid[h] == xj ? 1.0f : 0.0f;
+      w[h] = !kept[h] ? 0ull : (with_q ? fx40(fmaxf(p[h] - q, 0.0f)) : fx40(p[h]));
+    }
+    total = wave_add_u64(w[0] + w[1]);
+    if (total != 0ull) break;
+  }
+  int tok = -1;
+  if (total != 0ull) {
+    const uint64_t tp = canon::draw_point(uni[k], total);
+    // the first index (ascending) whose running sum exceeds tp, else the last index with
+    // weight: each weighted entry sums the weights at or below its index, the weighted
+    // entries in turn
+    typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    uint64_t* fw = F.tm[j];  // (the walk's masses are not needed any more)
+    int32_t* fi = F.idx[j];
+    const int n4 = (n + 3) & ~3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (lane + 64 * h < n4) fw[lane + 64 * h] = w[h];  // (pads: weight 0)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    uint64_t prefix[2] = {0ull, 0ull};
+    for (int q = 0; q < n4; q += 4) {
+      const i32x4 ii = *reinterpret_cast<const i32x4*>(fi + q);
+      const u64x2 wa = *reinterpret_cast<const u64x2*>(fw + q);
+      const u64x2 wb = *reinterpret_cast<const u64x2*>(fw + q + 2);
+      const uint64_t ww[4] = {wa[0], wa[1], wb[0], wb[1]};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) prefix[h] += ii[e] <= vid[h] ? ww[e] : 0ull;
+    }
+    int first = INT_MAX, last = -1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (w[h] != 0ull) {
+        if (prefix[h] > tp) first = min(first, (int)vid[h]);
+        last = max(last, (int)vid[h]);
+      }
+    first = wave_min_i32(first);
+    last = wave_max_i32(last);
+    tok = first != INT_MAX ? first : last;
+  }
+  if (lane <= k) {
+    int32_t o = -1;
+    if (lane < j) o = (int32_t)F.xid[lane];
+    else if (lane == j) o = tok;
+    ca.out_ids[trow0 + lane] = o;
+  }
+  if (lane == 0) {
+    ca.accepted[b] = __builtin_popcountll(acc_bits);
+    ca.emitted[b] = j;
+  }
+}
+
 // p'(x) for every element of every row (grid: rows x parts).
 template <int DT>
 __global__ void __launch_bounds__(kThreads) filtered_probs_kernel(const void* logits, int64_t V,
@@ -2044,6 +2586,46 @@ static bool filters_on(int top_k, float top_p, int64_t vocab) {
   return (top_k > 0 && (int64_t)top_k < vocab) || (top_p > 0.f && top_p < 1.f);
 }
 
+// The split path (each row over kParts workgroups, then one combine per row) takes few
+// rows of a vocabulary in its range, with a small top_k and 16-byte aligned rows.
+template <int DT>
+static bool split_applies(const void* a, const void* b, int64_t rows, int64_t V, int top_k) {
+  const int64_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
+  const bool aligned = (V * esz) % 16 == 0 && (uintptr_t)a % 16 == 0 &&
+                       (b == nullptr || (uintptr_t)b % 16 == 0);
+  const bool use_k = top_k > 0 && (int64_t)top_k < V;
+  return use_k && top_k <= filt::kDeferTopK && rows <= filt::kSplitMaxRows &&
+         V >= filt::kSplitMinVocab && V <= filt::kSplitMaxVocab && aligned;
+}
+
+// The split path's arguments: row infos and lists at the start of ws (as for
+// filter_rows_kernel), then lane states, part records and part lists.
+static filt::SplitArgs split_args(const void* a, int64_t n_a, const void* b, int64_t rows,
+                                  int64_t V, float c, int top_k, float top_p, void* ws) {
+  filt::SplitArgs sa;
+  sa.a = a;
+  sa.n_a = n_a;
+  sa.b = b;
+  sa.V = V;
+  sa.c = c;
+  sa.top_k = top_k;
+  sa.top_p = top_p;
+  sa.info = static_cast<filt::RowInfo*>(ws);
+  sa.lists = reinterpret_cast<int32_t*>(static_cast<char*>(ws) +
+                                        filt::align256(rows * (int64_t)sizeof(filt::RowInfo)));
+  char* base = static_cast<char*>(ws) + rows_ws_bytes(rows);
+  sa.lane_s = reinterpret_cast<float*>(base);
+  base += filt::align256(rows * canon::kLanes * 4);
+  sa.lane_r = reinterpret_cast<float*>(base);
+  base += filt::align256(rows * canon::kLanes * 4);
+  sa.parts = reinterpret_cast<filt::PartOut*>(base);
+  base += filt::align256(rows * filt::kParts * (int64_t)sizeof(filt::PartOut));
+  sa.ckeys = reinterpret_cast<uint32_t*>(base);
+  base += filt::align256(rows * filt::kParts * filt::kPartList * 4);
+  sa.cidx = reinterpret_cast<int32_t*>(base);
+  return sa;
+}
+
 template <int DT>
 static int launch_filter_rows(const void* a, int64_t n_a, const void* b, int64_t n_b, int64_t V,
                               float c, int top_k, float top_p, void* ws, hipStream_t st) {
@@ -2065,32 +2647,9 @@ static int launch_filter_rows(const void* a, int64_t n_a, const void* b, int64_t
   const bool use_p = top_p > 0.f && top_p < 1.f;
   ra.defer = (use_p && !use_k) || (use_k && top_k > filt::kDeferTopK);
   const int64_t rows = n_a + n_b;
-  const int64_t esz = DT == BSX_DTYPE_FP32 ? 4 : 2;
-  const bool aligned = (V * esz) % 16 == 0 && (uintptr_t)a % 16 == 0 &&
-                       (b == nullptr || (uintptr_t)b % 16 == 0);
-  if (use_k && top_k <= filt::kDeferTopK && rows <= filt::kSplitMaxRows &&
-      V >= filt::kSplitMinVocab && V <= filt::kSplitMaxVocab && aligned) {
+  if (split_applies<DT>(a, b, rows, V, top_k)) {
     // few rows: each row over kParts workgroups, then one combine per row
-    filt::SplitArgs sa;
-    sa.a = a;
-    sa.n_a = n_a;
-    sa.b = b;
-    sa.V = V;
-    sa.c = c;
-    sa.top_k = top_k;
-    sa.top_p = top_p;
-    sa.info = ra.info;
-    sa.lists = ra.lists;
-    char* base = static_cast<char*>(ws) + rows_ws_bytes(rows);
-    sa.lane_s = reinterpret_cast<float*>(base);
-    base += filt::align256(rows * canon::kLanes * 4);
-    sa.lane_r = reinterpret_cast<float*>(base);
-    base += filt::align256(rows * canon::kLanes * 4);
-    sa.parts = reinterpret_cast<filt::PartOut*>(base);
-    base += filt::align256(rows * filt::kParts * (int64_t)sizeof(filt::PartOut));
-    sa.ckeys = reinterpret_cast<uint32_t*>(base);
-    base += filt::align256(rows * filt::kParts * filt::kPartList * 4);
-    sa.cidx = reinterpret_cast<int32_t*>(base);
+    const filt::SplitArgs sa = split_args(a, n_a, b, rows, V, c, top_k, top_p, ws);
     hipLaunchKernelGGL((filt::filter_parts_kernel<DT>), dim3((unsigned)(rows * filt::kParts)),
                        dim3(filt::kThreads), 0, st, sa);
     BSX_LAUNCH_CHECK();
@@ -2115,6 +2674,21 @@ static int filtered_chain_impl(filt::ChainArgs& ca, void* ws, hipStream_t st, in
                                float top_p) {
   const int64_t n_t = (int64_t)ca.B * (ca.k + 1);
   const int64_t n_d = ca.d_logits ? (int64_t)ca.B * ca.k : 0;
+  if (ca.d_logits == nullptr && ca.k + 1 <= filt::kFastRows && top_k <= filt::kFastTopK &&
+      split_applies<DT>(ca.t_logits, nullptr, n_t, ca.V, top_k)) {
+    // few rows with one-hot drafts (the MTP engine's sampling verification): the parts,
+    // then the combine and the chain of each request in one workgroup
+    const filt::SplitArgs sa = split_args(ca.t_logits, n_t, nullptr, n_t, ca.V, ca.c, top_k,
+                                          top_p, ws);
+    ca.tiles_ready = 0;
+    hipLaunchKernelGGL((filt::filter_parts_kernel<DT>), dim3((unsigned)(n_t * filt::kParts)),
+                       dim3(filt::kThreads), 0, st, sa);
+    BSX_LAUNCH_CHECK();
+    hipLaunchKernelGGL((filt::filter_request_kernel<DT>), dim3((unsigned)ca.B),
+                       dim3(filt::kThreads), 0, st, sa, ca);
+    BSX_LAUNCH_CHECK();
+    return BSX_OK;
+  }
   int rc = launch_filter_rows<DT>(ca.t_logits, n_t, ca.d_logits, n_d, ca.V, ca.c, top_k, top_p,
                                   ws, st);
   if (rc != BSX_OK) return rc;

@@ -96,3 +96,34 @@ def test_split_rows_with_draft_logits_and_many_rows():
     ref = OAc.chain_filtered(d.float().numpy(), ids, t.float().numpy(), 1.0, 20, 0.95, u)
     for a, r in zip(got, ref):
         np.testing.assert_array_equal(a.cpu().numpy(), r)
+
+
+@pytest.mark.parametrize("k,top_k,top_p,sigma,quantize", [
+    (4, 20, 0.95, 2.0, 1.0),   # ties: parts that cannot list, requests on the fallback
+    (1, 20, 0.95, 2.0, None),
+    (3, 24, 0.0, 2.0, None),   # the largest top_k of the one-launch tail, top-k alone
+    (7, 5, 0.5, 8.0, None),    # eight rows (two per wave); peaked rows: the nucleus cuts first
+    (8, 20, 0.95, 2.0, None),  # nine rows: the combine and chain kernels instead
+    (2, 1, 0.0, 0.05, 64.0),   # top-1 with ties at the maximum
+])
+def test_one_hot_chain_on_the_request_kernel(k, top_k, top_p, sigma, quantize):
+    """One-hot drafts over split rows (the combine and the chain of each request in one
+    workgroup for k + 1 <= 8 and top_k <= 24), with draft ids out of range in some
+    requests, bit-exact against the oracle."""
+    say(f"split rows, one-hot chain: k={k} top_k={top_k} top_p={top_p} sigma={sigma} q={quantize}")
+    B, V = 12, 32000
+    x = _rows(B * (k + 1), V, torch.bfloat16, seed=100 + k, sigma=sigma, quantize=quantize)
+    t = x.reshape(B, k + 1, V)
+    rng = np.random.default_rng(k)
+    am = t.float().argmax(-1)[:, :k].numpy()
+    ids = np.where(rng.random((B, k)) < 0.7, am, rng.integers(0, V, (B, k))).astype(np.int64)
+    if k:
+        ids[1, 0] = -1
+        ids[2, k - 1] = V
+    u = rng.random((B, k + 1), dtype=np.float32)
+    got = S.chain_speculative_sampling_from_logits(None, torch.from_numpy(ids).to(DEV), t.to(DEV),
+                                                   0.6, uniforms=torch.from_numpy(u).to(DEV),
+                                                   top_k=top_k, top_p=top_p)
+    ref = OAc.chain_filtered(None, ids, t.float().numpy(), 0.6, top_k, top_p, u)
+    for a, r in zip(got, ref):
+        np.testing.assert_array_equal(a.cpu().numpy(), r)
