@@ -1115,6 +1115,268 @@ __global__ void __launch_bounds__(512) verify_attn_shared_kernel(Params p) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// ---- Wave-split tiles -----------------------------------------------------------------
+//
+// For batches of short views with at most 16 query rows per kv head (a draft token over a
+// sink + window view, say) and enough (request, kv head) pairs to fill the device: one
+// workgroup per pair, whose kSplitWaves waves split the request's visible tiles into
+// contiguous runs, each with its own online softmax, and combine them in LDS:
+//   o = sum_w 2^(m_w - M) o_w / sum_w 2^(m_w - M) l_w,  lse = M + log2(sum_w ...),
+// with M the largest reference maximum of the waves that saw a visible token.  No partial
+// leaves the workgroup, so no merge launch follows.  The tile step is the per-wave
+// kernel's (whole-line K loads, V rows transposed in registers, the next tile's loads
+// issued as soon as its registers are free); every tile is masked (causal, sink +
+// window, kv end).
+using attn_shape::kSplitWaves;
+
+template <int DT, int D>
+__global__ void __launch_bounds__(64 * kSplitWaves) verify_attn_wsplit_kernel(Params p) {
+  constexpr int NT = 1;
+  constexpr int KS = D / 32;  // k-steps of the QK^T contraction
+  constexpr int NJ = D / 16;  // output d tiles
+  constexpr int VW = NJ / 2;  // dwords per lane per token of a V row
+  constexpr int W = kSplitWaves;
+  constexpr int FR = 4 * NJ;  // output floats per lane
+  // [wave][fragment element][lane]: each store and read covers 64 consecutive floats
+  __shared__ float o_lds[W][FR][64];
+  __shared__ float m_lds[W][64], l_lds[W][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = uni(threadIdx.x >> 6);
+  const int c16 = lane & 15;
+  const int g4 = lane >> 4;
+  const int h = blockIdx.y;
+  Seg cur;
+  {
+    const int32_t* sq = p.blob + p.off_seq + 4 * blockIdx.x;
+    cur.b = blockIdx.x;
+    cur.qo_start = ld_uniform(sq, 0);
+    cur.qo_len = ld_uniform(sq, 1);
+    cur.kv_len = ld_uniform(sq, 2);
+    cur.page_start = ld_uniform(sq, 3);
+    cur.slot = -1;
+    cur.t0 = 0;
+    cur.t1 = 0;
+  }
+  if (cur.qo_len == 0) return;  // (the whole workgroup)
+  const int g = p.group;
+  const uint32_t tok_bytes = (uint32_t)(p.num_kv_heads * D * 2);
+  const uint32_t head_off = (uint32_t)(h * D * 2);
+
+  // The layer's appended rows of this request and kv head, written before any load
+  // (the stores complete before the barrier).
+  if (p.k_new != nullptr) {
+    constexpr int PIECES = D * 2 / 16;  // 16-byte pieces of a row's head slice
+    const int diag0 = cur.kv_len - cur.qo_len;
+    for (int idx = threadIdx.x; idx < cur.qo_len * PIECES; idx += blockDim.x) {
+      const int i = idx / PIECES;
+      const int pos = diag0 + i;
+      if (pos < 0) continue;
+      const int64_t col = (int64_t)head_off + (int64_t)(idx - i * PIECES) * 16;
+      const int page = p.kv_indices[cur.page_start + (pos >> p.page_shift)];
+      const int64_t dst = (int64_t)page * p.page_stride_bytes +
+                          (int64_t)(pos & p.page_mask) * tok_bytes + col;
+      const int64_t src = cur.qo_start + i;
+      const u32x4 kv = *reinterpret_cast<const u32x4*>(
+          reinterpret_cast<const char*>(p.k_new + src * p.knew_stride) + col);
+      const u32x4 vv = *reinterpret_cast<const u32x4*>(
+          reinterpret_cast<const char*>(p.v_new + src * p.vnew_stride) + col);
+      *reinterpret_cast<u32x4*>(const_cast<char*>(p.k_cache) + dst) = kv;
+      *reinterpret_cast<u32x4*>(const_cast<char*>(p.v_cache) + dst) = vv;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+  // The visible tiles [0, a_end) and [w_beg, ntiles) (one run unless a sink + window view
+  // leaves a gap), and this wave's run of them.
+  const int ntiles = (cur.kv_len + kTile - 1) / kTile;
+  int a_end = ntiles, w_beg = ntiles;
+  if (p.mask_mode == BSX_MASK_STREAMING && cur.kv_len > p.sink + p.window) {
+    const int ae = (p.sink + kTile - 1) / kTile;
+    const int wb = max(0, cur.kv_len - p.window) / kTile;
+    if (wb > ae) {
+      a_end = ae;
+      w_beg = wb;
+    }
+  }
+  const int T = a_end + (ntiles - w_beg);
+  const int i0 = (int)((int64_t)T * wave / W);
+  const int i1 = (int)((int64_t)T * (wave + 1) / W);
+  auto tile_of = [&](int i) { return i < a_end ? i : w_beg + (i - a_end); };
+
+  const int nrows = cur.qo_len * g;  // <= 16 (the planner's condition)
+  const int diag = cur.kv_len - cur.qo_len;
+  const int sink_end = p.mask_mode == BSX_MASK_STREAMING ? p.sink : cur.kv_len;
+  const int win_beg = p.mask_mode == BSX_MASK_STREAMING ? cur.kv_len - p.window : cur.kv_len;
+  RowMask rm[NT];
+  row_masks<NT>(p, cur, 0, c16, rm);
+  // Q (B operand of S^T = K Q^T): lane holds query row c16, d chunk (s, g4); padded rows
+  // read row 0 (finite data; their results are never stored)
+  u32x4 qr[KS];
+  {
+    const bool rv = c16 < nrows;
+    const int tq = rv ? c16 / g : 0;
+    const int hh = rv ? c16 - tq * g : 0;
+    const uint16_t* qp =
+        p.q + (int64_t)(cur.qo_start + tq) * p.q_stride + (int64_t)(h * g + hh) * D;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 32 * s + 8 * g4);
+  }
+
+  // Tile loads (page size >= 16: a 16-token subtile lies in one page).  K: whole
+  // 128-byte lines (token (c16 & 7) + 8 h, bytes 128 q + 16 (g4 + 4 (c16 >> 3))), moved
+  // into the A layout by a row rotation; V: 8 token rows per lane.
+  u32x4 kreg[2][KS];
+  uint32_t vraw[8][VW];
+  const int ktok = c16 & 7;
+  const uint32_t kbyte = (uint32_t)(16 * (g4 + 4 * (c16 >> 3)));
+  auto page_of = [&](int js) {
+    const int jsc = js < cur.kv_len ? js : 0;
+    return ld_uniform(p.kv_indices, cur.page_start + (jsc >> p.page_shift));
+  };
+  auto load_tile_k = [&](int tile) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int js = tile * kTile + 16 * st;
+      const int jsc = js < cur.kv_len ? js : 0;
+      const char* base = p.k_cache + (int64_t)page_of(js) * p.page_stride_bytes;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint32_t off =
+            (uint32_t)(((jsc & p.page_mask) + ktok + 8 * hh) * tok_bytes) + head_off + kbyte;
+#pragma unroll
+        for (int q = 0; q < KS / 2; ++q) kreg[st][2 * q + hh] = ld_stream(base + off + 128 * q);
+      }
+    }
+  };
+  const bool klow = c16 < 8;
+  auto kfix = [&](u32x4 (&a)[2][KS]) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int q = 0; q < KS / 2; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t x0 = kreg[st][2 * q][e], x1 = kreg[st][2 * q + 1][e];
+          const uint32_t r0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)x0, 0x128, 0xf, 0xf, false);
+          const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)x1, 0x128, 0xf, 0xf, false);
+          a[st][2 * q][e] = klow ? x0 : r1;
+          a[st][2 * q + 1][e] = klow ? r0 : x1;
+        }
+  };
+  auto load_tile_v = [&](int tile) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int js = tile * kTile + 16 * st;
+      const int jsc = js < cur.kv_len ? js : 0;
+      const char* base = p.v_cache + (int64_t)page_of(js) * p.page_stride_bytes;
+      const uint32_t soff = (uint32_t)((jsc & p.page_mask) * tok_bytes) + head_off;
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int e = 4 * st + e4;
+        const uint32_t off = soff + (uint32_t)((4 * g4 + e4) * tok_bytes) + (uint32_t)(NJ * c16 * 2);
+        if constexpr (VW == 4) {
+          const u32x4 v = ld_stream(base + off);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) vraw[e][w] = v[w];
+        } else {
+          const u32x2 v = ld_stream2(base + off);
+          vraw[e][0] = v[0];
+          vraw[e][1] = v[1];
+        }
+      }
+    }
+  };
+
+  f32x4 o[NJ][NT];
+#pragma unroll
+  for (int jm = 0; jm < NJ; ++jm) o[jm][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_ref[NT] = {-INFINITY};
+  float l_run[NT] = {0.f};
+  auto tile_step = [&](int i, auto prefetch_tag) {
+    constexpr bool PREFETCH = decltype(prefetch_tag)::value;
+    const int j0 = tile_of(i) * kTile;
+    const int nxt = tile_of(i + 1);
+    u32x4 kop[2][KS];
+    kfix(kop);
+    f32x4 sacc[2][NT];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) acc = mfma16x16x32<DT>(kop[st][s], qr[s], acc);
+      sacc[st][0] = acc;
+    }
+    // K registers are free: the next tile's K (kept after their last reads, so the
+    // loaded tile lands in place)
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PREFETCH) load_tile_k(nxt);
+    mask_tile<NT>(sacc, rm, j0, g4, diag, sink_end, win_beg);
+    uint32_t pb[NT][4];
+    softmax_tile<DT, NJ, NT>(sacc, p.scale_log2, m_ref, l_run, o, pb);
+    zero_rows_past_end<VW>(vraw, j0, g4, cur.kv_len);
+    u32x4 va[NJ];
+    transpose_v<NJ, VW>(vraw, va);
+#pragma unroll
+    for (int jm = 0; jm < NJ; ++jm) asm volatile("" ::"v"(va[jm]) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PREFETCH) load_tile_v(nxt);  // V registers are free
+    pv_tile<DT, NJ, NT>(va, pb, o);
+  };
+  if (i0 < i1) {
+    load_tile_k(tile_of(i0));
+    load_tile_v(tile_of(i0));
+    for (int i = i0; i + 1 < i1; ++i) tile_step(i, std::true_type());
+    tile_step(i1 - 1, std::false_type());  // the run's last tile: nothing to prefetch
+  }
+
+  // Combine the waves' runs in LDS (the first wave normalises and stores).
+  float l = l_run[0];
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+#pragma unroll
+  for (int jm = 0; jm < NJ; ++jm)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o_lds[wave][4 * jm + e][lane] = o[jm][0][e];
+  m_lds[wave][lane] = m_ref[0];
+  l_lds[wave][lane] = l;
+  __syncthreads();
+  if (wave != 0) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < W; ++w)
+    if (l_lds[w][lane] > 0.f) M = fmaxf(M, m_lds[w][lane]);
+  float f[W];
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const float lw = l_lds[w][lane];
+    f[w] = lw > 0.f ? __builtin_amdgcn_exp2f(m_lds[w][lane] - M) : 0.f;
+    L += f[w] * lw;
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  f32x4 oc[NJ][NT];
+#pragma unroll
+  for (int jm = 0; jm < NJ; ++jm)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) acc += f[w] * o_lds[w][4 * jm + e][lane];
+      oc[jm][0][e] = acc * inv;
+    }
+  if (c16 < nrows) {
+    const int tq = c16 / g;
+    const int hh = c16 - tq * g;
+    uint16_t* op = p.out + (int64_t)(cur.qo_start + tq) * p.out_stride + (int64_t)(h * g + hh) * D;
+    store_row<DT, D, NT, true>(op, g4, oc, 0);
+    if (p.lse_out != nullptr && g4 == 0)
+      p.lse_out[(int64_t)(cur.qo_start + tq) * p.num_qo_heads + h * g + hh] =
+          (L > 0.f ? M + __log2f(L) : -INFINITY) * 0.69314718055994531f;
+  }
+}
+
 // Combine the partial results of split requests: o = sum_p w_p o_p / sum_p w_p with
 // w_p = 2^(lse_p - max lse), parts in slot order.  grid (split request, kv head, row
 // chunk); one thread per (query row, 4 output columns).  The lse and o of up to U
@@ -1229,6 +1491,13 @@ static int launch_all(const bsx_attn_plan_t* plan, const Params& prm, hipStream_
     BSX_LAUNCH_CHECK();
     return BSX_OK;
   }
+  if (plan->shared_kv_tiles == attn_shape::kPlanWaveSplit) {
+    // one workgroup per (request, kv head); the waves merge in LDS: no merge launch
+    hipLaunchKernelGGL((verify_attn_wsplit_kernel<DT, D>),
+                       dim3(plan->batch, plan->num_kv_heads), dim3(64 * kSplitWaves), 0, st, prm);
+    BSX_LAUNCH_CHECK();
+    return BSX_OK;
+  }
   const int waves = plan->heads_per_cta * prm.qblocks_per_cta;
   const bool ps16 = plan->page_size >= 16;
   int rc;
@@ -1290,7 +1559,13 @@ static int attn_run_impl(const bsx_attn_plan_t* plan, const int32_t* plan_blob_d
                   plan->heads_per_cta * plan->qblocks_per_cta <= 8 &&
                   plan->num_qgroups * plan->qblocks_per_cta >= plan->qrow_blocks,
               BSX_ERR_INVALID, "inconsistent plan (workgroup shape)");
-  if (plan->shared_kv_tiles) {
+  if (plan->shared_kv_tiles == attn_shape::kPlanWaveSplit) {
+    BSX_REQUIRE(plan->qrow_tile == 16 && plan->qrow_blocks == 1 && plan->page_size >= 16 &&
+                    !plan->device_plan &&
+                    (plan->mask_mode == BSX_MASK_NONE || plan->mask_mode == BSX_MASK_CAUSAL ||
+                     plan->mask_mode == BSX_MASK_STREAMING),
+                BSX_ERR_INVALID, "inconsistent plan (wave-split tiles)");
+  } else if (plan->shared_kv_tiles) {
     const int qb = plan->qblocks_per_cta;
     BSX_REQUIRE((qb == 2 || qb == 4 || qb == 8) && plan->qrow_tile == 32 &&
                     plan->page_size >= 16 &&

@@ -31,5 +31,15 @@ constexpr int shared_lds_bytes(int head_dim, int qb) {
   return shared_stages(head_dim, qb) * shared_max_heads(head_dim, qb) * head_tile_bytes(head_dim);
 }
 
+// Wave-split kernel (bsx_attn_plan_t.shared_kv_tiles == kPlanWaveSplit): one workgroup
+// of kSplitWaves waves per (request, kv head), the waves splitting the request's visible
+// tiles and merging in LDS.  Planned for at most 16 query rows per kv head, pages of 16+
+// tokens, causal / no / sink + window masks, when the (request, kv head) pairs fill the
+// compute units and no request has more than kSplitMaxTiles visible tiles (a few per
+// wave: the workgroup, not a segment, is then the unit of balance).
+constexpr int kPlanWaveSplit = 2;
+constexpr int kSplitWaves = 8;
+constexpr int kSplitMaxTiles = 4 * kSplitWaves;
+
 }  // namespace attn_shape
 }  // namespace bsx

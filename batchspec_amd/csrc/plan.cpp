@@ -312,6 +312,31 @@ static void write_blob(const HostSchedule& hs, const int32_t* qo_indptr_h,
   PLAN_REQUIRE(mask_mode != BSX_MASK_STREAMING || (sink_tokens >= 0 && window_tokens >= 0),     \
                BSX_ERR_INVALID, "streaming view needs sink >= 0 and window >= 0")
 
+// The wave-split kernel fits: at most 16 query rows per kv head (one 16-row tile), pages
+// of 16 or more tokens, a causal / no / sink + window mask, (request, kv head) pairs that
+// fill the compute units, and no request with more than kSplitMaxTiles visible tiles.
+static bool wave_split_fits(const HostSchedule& hs, const GridShape& gs, int batch,
+                            int num_kv_heads, int page_size, int mask_mode, int sink_tokens,
+                            int window_tokens, int num_cus) {
+  if (gs.shared || gs.qrow_tile != 16 || gs.qrow_blocks != 1 || page_size < 16) return false;
+  if (mask_mode != BSX_MASK_NONE && mask_mode != BSX_MASK_CAUSAL &&
+      mask_mode != BSX_MASK_STREAMING)
+    return false;
+  if ((int64_t)batch * num_kv_heads < num_cus) return false;
+  for (int b = 0; b < batch; ++b) {
+    const int kl = hs.kv_len[b];
+    const int ntiles = (kl + kTileTokens - 1) / kTileTokens;
+    int visible = ntiles;
+    if (mask_mode == BSX_MASK_STREAMING && kl > sink_tokens + window_tokens) {
+      const int a_end = (sink_tokens + kTileTokens - 1) / kTileTokens;
+      const int w_beg = std::max(0, kl - window_tokens) / kTileTokens;
+      if (w_beg > a_end) visible = a_end + (ntiles - w_beg);
+    }
+    if (visible > bsx::attn_shape::kSplitMaxTiles) return false;
+  }
+  return true;
+}
+
 extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
                              const int32_t* kv_last_page_len_h, int batch, int num_qo_heads,
                              int num_kv_heads, int head_dim, int page_size, int mask_mode,
@@ -383,6 +408,19 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   out->total_tiles = hs.total_tiles;
   out->shared_kv_tiles = gs.shared ? 1 : 0;
   out->off_dyn = -1;
+  if (wave_split_fits(hs, gs, batch, num_kv_heads, page_size, mask_mode, sink_tokens,
+                      window_tokens, num_cus)) {
+    // one workgroup per (request, kv head), its waves merging in LDS: no partials, no
+    // merge launch (the blob keeps its request records; the segments go unused)
+    out->shared_kv_tiles = bsx::attn_shape::kPlanWaveSplit;
+    out->heads_per_cta = 1;
+    out->qblocks_per_cta = 1;
+    out->num_qgroups = 1;
+    out->num_ctas = batch;
+    out->num_partials = 0;
+    out->num_split_requests = 0;
+    out->float_ws_bytes = 0;
+  }
   return BSX_OK;
 }
 

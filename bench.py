@@ -160,11 +160,22 @@ def pass_record(wr, us, nbytes):
     p = wr[0].plan_info
     return {"us": round(t, 2), "us_median": round(median(us), 2), "GB/s": round(nbytes / t / 1e3, 1),
             "frac": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "bytes": int(nbytes),
-            "plan": {"workgroups": int(p.num_ctas), "segments": int(p.num_segments),
-                     "split_requests": int(p.num_split_requests),
-                     "shared_kv_tiles": int(p.shared_kv_tiles),
-                     "heads_per_workgroup": int(p.heads_per_cta),
-                     "waves_per_head": int(p.qblocks_per_cta)}}
+            "plan": plan_record(p)}
+
+
+ATTN_KERNELS = {0: "verify_attn_kernel (per-wave tiles)",
+                1: "verify_attn_shared_kernel (K/V tiles shared through LDS)",
+                2: "verify_attn_wsplit_kernel (one workgroup per request and kv head, waves "
+                   "merged in LDS)"}
+
+
+def plan_record(p):
+    """The launch shape of an attention plan: the whole grid, the kernel, the split."""
+    grid = int(p.num_ctas) * (int(p.num_kv_heads) // int(p.heads_per_cta)) * int(p.num_qgroups)
+    return {"workgroups": grid, "kernel": ATTN_KERNELS[int(p.shared_kv_tiles)],
+            "segments": int(p.num_segments), "split_requests": int(p.num_split_requests),
+            "shared_kv_tiles": int(p.shared_kv_tiles), "heads_per_workgroup": int(p.heads_per_cta),
+            "waves_per_head": int(p.qblocks_per_cta)}
 
 
 def spaced_runs(wr, sets, iters, gap_cycles=400_000):
@@ -809,8 +820,7 @@ def main() -> int:
         "append_attention_fused_us": round(mean(fused_us), 2),
         "append_GBs": round(mean(pbytes) / t_app / 1e3, 1),
         "attn_bytes": int(a_bytes),
-        "plan": {"workgroups": int(p0.num_ctas), "segments": int(p0.num_segments),
-                 "split_requests": int(p0.num_split_requests), "tiles": int(p0.total_tiles)},
+        "plan": dict(plan_record(p0), tiles=int(p0.total_tiles)),
         "wall_s": round(wall, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),

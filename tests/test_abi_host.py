@@ -219,3 +219,30 @@ def test_product_has_no_cpu_path():
         bsx.get_seq_lens(torch.zeros(3, dtype=torch.int32), torch.zeros(2, dtype=torch.int32), 16)
     with pytest.raises(ValueError, match="no CPU path"):
         bsx.BatchPrefillWithPagedKVCacheWrapper(torch.empty(1024, dtype=torch.uint8))
+
+
+def test_plan_wave_split_for_short_views_that_fill_the_device():
+    """The host planner takes the wave-split kernel (shared_kv_tiles 2: one workgroup per
+    request and kv head, no partials) when every view has at most 32 tiles, a kv head has
+    at most 16 query rows and the (request, kv head) pairs fill the compute units; any
+    other shape keeps the split-KV schedule."""
+    B = 32
+    rng = np.random.default_rng(0)
+    ctx = rng.integers(32768, 65536, B)
+    pages = -(-(ctx + 1) // 16)
+    kvp = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    last = ((ctx + 1 - 1) % 16 + 1).astype(np.int32)
+    qo = np.arange(B + 1, dtype=np.int32)  # one query token each
+    # config 3a: a 64-sink + 512-window view (19 tiles) of 32k-64k tokens, 32 x 8 pairs
+    p, _ = _plan(qo, kvp, last, mode=_lib.MASK_STREAMING, sink=64, window=512)
+    assert p.shared_kv_tiles == 2 and p.num_partials == 0 and p.num_split_requests == 0
+    assert p.float_ws_bytes == 0 and p.num_ctas == B and p.heads_per_cta == 1
+    # the full causal view (1000+ tiles), fewer pairs than units, 5 query tokens x 4:
+    # split-KV
+    p, _ = _plan(qo, kvp, last, mode=_lib.MASK_CAUSAL)
+    assert p.shared_kv_tiles != 2
+    p, _ = _plan(qo, kvp, last, mode=_lib.MASK_STREAMING, sink=64, window=512, cus=512)
+    assert p.shared_kv_tiles != 2
+    qo5 = np.arange(B + 1, dtype=np.int32) * 5
+    p, _ = _plan(qo5, kvp, last, mode=_lib.MASK_STREAMING, sink=64, window=512)
+    assert p.shared_kv_tiles != 2

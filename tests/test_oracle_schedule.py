@@ -67,15 +67,19 @@ def test_device_shape_layout(B, hq, hkv, d, max_qo, mode):
             plan.off_dyn, plan.plan_ints) == (L["off_seg_indptr"], L["off_segments"], L["off_merge"],
                                               L["off_part"], L["off_dyn"], L["ints"])
     assert plan.off_merge_seqs % 4 == 0 and plan.num_split_requests == B
-    # the same workgroup shape as a host plan whose longest request has max_qo tokens
+    # the same workgroup shape as a host plan whose longest request has max_qo tokens (on
+    # more compute units than (request, kv head) pairs: the host-only wave-split kernel,
+    # which a device plan never takes, needs the pairs to fill the device; the shape
+    # compared does not depend on the unit count)
     qo = np.arange(B + 1, dtype=np.int32) * max_qo
     kvp = np.arange(B + 1, dtype=np.int32) * 4
     last = np.full(B, 16, np.int32)
-    bound = int(lib.bsx_attn_plan_ints_bound(B, 256))
+    cus = B * hkv + 1
+    bound = int(lib.bsx_attn_plan_ints_bound(B, cus))
     blob = np.empty(bound, np.int32)
     hp = _lib.AttnPlan()
     rc = lib.bsx_attn_plan(qo.ctypes.data, kvp.ctypes.data, last.ctypes.data, B, hq, hkv, d, 16,
-                           mode, 64 if mode == 3 else 0, 512 if mode == 3 else 0, 0.0, 256, -1,
+                           mode, 64 if mode == 3 else 0, 512 if mode == 3 else 0, 0.0, cus, -1,
                            blob.ctypes.data, bound, ctypes.byref(hp))
     assert rc == 0
     for f in ("qrow_tile", "qrow_blocks", "heads_per_cta", "qblocks_per_cta", "num_qgroups",
