@@ -1140,6 +1140,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) verify_attn_wsplit_kernel(Pa
   // [wave][fragment element][lane]: each store and read covers 64 consecutive floats
   __shared__ float o_lds[W][FR][64];
   __shared__ float m_lds[W][64], l_lds[W][64];
+  __shared__ float oc_lds[FR][64];  // the combined, normalised output
 
   const int lane = threadIdx.x & 63;
   const int wave = uni(threadIdx.x >> 6);
@@ -1331,7 +1332,8 @@ __global__ void __launch_bounds__(64 * kSplitWaves) verify_attn_wsplit_kernel(Pa
     tile_step(i1 - 1, std::false_type());  // the run's last tile: nothing to prefetch
   }
 
-  // Combine the waves' runs in LDS (the first wave normalises and stores).
+  // Combine the waves' runs in LDS: wave w combines and normalises output d-tiles w,
+  // w + W, ... of every run into oc_lds, then the first wave stores the rows.
   float l = l_run[0];
   l += __shfl_xor(l, 16);
   l += __shfl_xor(l, 32);
@@ -1342,7 +1344,6 @@ __global__ void __launch_bounds__(64 * kSplitWaves) verify_attn_wsplit_kernel(Pa
   m_lds[wave][lane] = m_ref[0];
   l_lds[wave][lane] = l;
   __syncthreads();
-  if (wave != 0) return;
   float M = -INFINITY;
 #pragma unroll
   for (int w = 0; w < W; ++w)
@@ -1356,16 +1357,21 @@ __global__ void __launch_bounds__(64 * kSplitWaves) verify_attn_wsplit_kernel(Pa
     L += f[w] * lw;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  f32x4 oc[NJ][NT];
-#pragma unroll
-  for (int jm = 0; jm < NJ; ++jm)
+  for (int jm = wave; jm < NJ; jm += W)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float acc = 0.f;
 #pragma unroll
       for (int w = 0; w < W; ++w) acc += f[w] * o_lds[w][4 * jm + e][lane];
-      oc[jm][0][e] = acc * inv;
+      oc_lds[4 * jm + e][lane] = acc * inv;
     }
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 oc[NJ][NT];
+#pragma unroll
+  for (int jm = 0; jm < NJ; ++jm)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) oc[jm][0][e] = oc_lds[4 * jm + e][lane];
   if (c16 < nrows) {
     const int tq = c16 / g;
     const int hh = c16 - tq * g;
