@@ -103,7 +103,10 @@ typedef struct {
                              when the page table holds no page               */
   int32_t shared_kv_tiles;/* 1: the qblocks_per_cta waves of a kv head share
                              each K/V tile through LDS (many query rows per
-                             kv head); 0: every wave streams its own tiles   */
+                             kv head); 0: every wave streams its own tiles;
+                             2: one workgroup per (request, kv head), its
+                             waves splitting the request's tiles and merging
+                             in LDS (grid batch x num_kv_heads, no partials) */
   int64_t total_tiles;    /* kv tiles of the whole schedule                   */
   int32_t device_plan;    /* 1: the blob is written on the device by
                              bsx_attn_plan_device; counts above are bounds    */
