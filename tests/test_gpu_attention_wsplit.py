@@ -177,3 +177,40 @@ def test_fused_append_equals_append_then_run():
         o1, l1 = w.run(s.q, c_one, return_lse=True, append_key=s.k_new, append_value=s.v_new)
         torch.cuda.synchronize()
         assert torch.equal(o1, o2) and torch.equal(l1, l2) and torch.equal(c_one, c_two)
+
+
+@pytest.mark.parametrize("dtype,D,Hq,Hkv", [(torch.float16, 128, 32, 8), (torch.bfloat16, 64, 16, 8),
+                                            (torch.float16, 64, 32, 8)])
+def test_sink_window_dtypes_and_head_dims(dtype, D, Hq, Hkv):
+    say(f"wave split: sink + window view, {dtype} D={D} H={Hq}/{Hkv}")
+    b = make_verify_batch(32, 2000, 6000, 1, Hq, Hkv, D, 16, dtype=dtype, seed=D + Hq).to(DEV)
+    w = _plan(b, causal=True, sink_tokens=64, window_tokens=512)
+    _assert_wave_split(w)
+    _check(b, w, "streaming", sink=64, window=512)
+
+
+def test_captured_run_replays():
+    """run() on a wave-split plan captured in a CUDA graph: each replay, with new q and
+    cache contents written between replays, equals the eager run on the same inputs."""
+    say("wave split: captured run() replays")
+    b = make_verify_batch(64, 100, 1000, 2, 32, 8, 128, 16, dtype=torch.bfloat16, seed=5).to(DEV)
+    w = _plan(b, causal=True)
+    _assert_wave_split(w)
+    q = b.q.clone()
+    cache = b.cache.clone()
+    out = torch.empty_like(q)
+    w.run(q, cache, out=out)  # warm up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        w.run(q, cache, out=out)
+    gen = torch.Generator(device="cpu").manual_seed(11)
+    for rep in range(4):
+        q.copy_((torch.randn(q.shape, generator=gen) * 0.5).to(q.dtype))
+        cache.copy_((torch.randn(cache.shape, generator=gen) * 0.5).to(cache.dtype))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = w.run(q, cache)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {rep} differs from the eager run"
