@@ -34,12 +34,31 @@ constexpr int shared_lds_bytes(int head_dim, int qb) {
 // Wave-split kernel (bsx_attn_plan_t.shared_kv_tiles == kPlanWaveSplit): one workgroup
 // of kSplitWaves waves per (request, kv head), the waves splitting the request's visible
 // tiles and merging in LDS.  Planned for at most 16 query rows per kv head, pages of 16+
-// tokens, causal / no / sink + window masks, when the (request, kv head) pairs fill the
-// compute units and no request has more than kSplitMaxTiles visible tiles (a few per
-// wave: the workgroup, not a segment, is then the unit of balance).
+// tokens, causal / no / sink + window masks, no request with more than kSplitMaxTiles
+// visible tiles, and between half the compute units and all of them in (request, kv
+// head) pairs, when the time model below puts it ahead of the split-KV schedule.
 constexpr int kPlanWaveSplit = 2;
 constexpr int kSplitWaves = 8;
 constexpr int kSplitMaxTiles = 4 * kSplitWaves;
+
+// Time model of the two schedules in microseconds, fitted on MI355X to the measured
+// kernel times (head dim 128, bf16) of decode and 4-token draft batches with 128..512
+// (request, kv head) pairs and views of 10..32 tiles; MB = visible K/V bytes / 1e6.
+//   wave-split: max(kWsLatencyUs + kWsWaveTileUs * (longest view's tiles) / kSplitWaves,
+//                   kWsFixedUs + kWsUsPerMB * MB)
+//     the longest view's run per wave, or the workgroups' streaming (5.5 TB/s)
+//   split-KV:   kSkFixedUs + kSkUsPerMB * MB + kSkRowUs * (query rows per kv head - 4)
+//     the merge launch and partials, the balanced stream (7.0 TB/s), the partial rows
+// Above one workgroup per compute unit the wave-split kernel's two co-resident
+// workgroups per unit fall behind the balanced split (measured 4-36% slower at 288-2048
+// pairs, except sink + window views within 5%), so it is not planned there.
+constexpr double kWsLatencyUs = 7.55;
+constexpr double kWsWaveTileUs = 3.47;
+constexpr double kWsFixedUs = 6.25;
+constexpr double kWsUsPerMB = 0.182;
+constexpr double kSkFixedUs = 11.81;
+constexpr double kSkUsPerMB = 0.143;
+constexpr double kSkRowUs = 0.294;
 
 }  // namespace attn_shape
 }  // namespace bsx

@@ -316,13 +316,17 @@ static void write_blob(const HostSchedule& hs, const int32_t* qo_indptr_h,
 // of 16 or more tokens, a causal / no / sink + window mask, (request, kv head) pairs that
 // fill the compute units, and no request with more than kSplitMaxTiles visible tiles.
 static bool wave_split_fits(const HostSchedule& hs, const GridShape& gs, int batch,
-                            int num_kv_heads, int page_size, int mask_mode, int sink_tokens,
-                            int window_tokens, int num_cus) {
+                            int num_kv_heads, int group, int head_dim, int page_size,
+                            int mask_mode, int sink_tokens, int window_tokens, int num_cus) {
+  namespace as = bsx::attn_shape;
   if (gs.shared || gs.qrow_tile != 16 || gs.qrow_blocks != 1 || page_size < 16) return false;
   if (mask_mode != BSX_MASK_NONE && mask_mode != BSX_MASK_CAUSAL &&
       mask_mode != BSX_MASK_STREAMING)
     return false;
-  if ((int64_t)batch * num_kv_heads < num_cus) return false;
+  const int64_t pairs = (int64_t)batch * num_kv_heads;
+  if (2 * pairs < num_cus || pairs > num_cus) return false;
+  int longest = 0;
+  int64_t tiles = 0;
   for (int b = 0; b < batch; ++b) {
     const int kl = hs.kv_len[b];
     const int ntiles = (kl + kTileTokens - 1) / kTileTokens;
@@ -332,9 +336,18 @@ static bool wave_split_fits(const HostSchedule& hs, const GridShape& gs, int bat
       const int w_beg = std::max(0, kl - window_tokens) / kTileTokens;
       if (w_beg > a_end) visible = a_end + (ntiles - w_beg);
     }
-    if (visible > bsx::attn_shape::kSplitMaxTiles) return false;
+    if (visible > as::kSplitMaxTiles) return false;
+    if (hs.qo_len[b] > 0) {
+      longest = std::max(longest, visible);
+      tiles += visible;
+    }
   }
-  return true;
+  const double mb = (double)tiles * num_kv_heads * as::head_tile_bytes(head_dim) * 1e-6;
+  const double ws_us = std::max(as::kWsLatencyUs + as::kWsWaveTileUs * longest / as::kSplitWaves,
+                                as::kWsFixedUs + as::kWsUsPerMB * mb);
+  const double sk_us = as::kSkFixedUs + as::kSkUsPerMB * mb +
+                       as::kSkRowUs * std::max(0, hs.max_qo * group - 4);
+  return ws_us < sk_us;
 }
 
 extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
@@ -408,8 +421,8 @@ extern "C" int bsx_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indpt
   out->total_tiles = hs.total_tiles;
   out->shared_kv_tiles = gs.shared ? 1 : 0;
   out->off_dyn = -1;
-  if (wave_split_fits(hs, gs, batch, num_kv_heads, page_size, mask_mode, sink_tokens,
-                      window_tokens, num_cus)) {
+  if (wave_split_fits(hs, gs, batch, num_kv_heads, group, head_dim, page_size, mask_mode,
+                      sink_tokens, window_tokens, num_cus)) {
     // one workgroup per (request, kv head), its waves merging in LDS: no partials, no
     // merge launch (the blob keeps its request records; the segments go unused)
     out->shared_kv_tiles = bsx::attn_shape::kPlanWaveSplit;

@@ -224,8 +224,9 @@ def test_product_has_no_cpu_path():
 def test_plan_wave_split_for_short_views_that_fill_the_device():
     """The host planner takes the wave-split kernel (shared_kv_tiles 2: one workgroup per
     request and kv head, no partials) when every view has at most 32 tiles, a kv head has
-    at most 16 query rows and the (request, kv head) pairs fill the compute units; any
-    other shape keeps the split-KV schedule."""
+    at most 16 query rows, the (request, kv head) pairs number between half the compute
+    units and all of them, and its time model puts it ahead of the split-KV schedule;
+    any other shape keeps the split-KV schedule."""
     B = 32
     rng = np.random.default_rng(0)
     ctx = rng.integers(32768, 65536, B)
@@ -237,12 +238,31 @@ def test_plan_wave_split_for_short_views_that_fill_the_device():
     p, _ = _plan(qo, kvp, last, mode=_lib.MASK_STREAMING, sink=64, window=512)
     assert p.shared_kv_tiles == 2 and p.num_partials == 0 and p.num_split_requests == 0
     assert p.float_ws_bytes == 0 and p.num_ctas == B and p.heads_per_cta == 1
-    # the full causal view (1000+ tiles), fewer pairs than units, 5 query tokens x 4:
-    # split-KV
-    p, _ = _plan(qo, kvp, last, mode=_lib.MASK_CAUSAL)
-    assert p.shared_kv_tiles != 2
+    # down to half the units (256 pairs on 512), then no further
     p, _ = _plan(qo, kvp, last, mode=_lib.MASK_STREAMING, sink=64, window=512, cus=512)
+    assert p.shared_kv_tiles == 2
+    p, _ = _plan(qo, kvp, last, mode=_lib.MASK_STREAMING, sink=64, window=512, cus=513)
+    assert p.shared_kv_tiles != 2
+    # more pairs than units: two workgroups per unit fall behind the balanced split
+    p, _ = _plan(qo, kvp, last, mode=_lib.MASK_STREAMING, sink=64, window=512, cus=255)
+    assert p.shared_kv_tiles != 2
+    # the full causal view (1000+ tiles), 5 query tokens x 4 rows: split-KV
+    p, _ = _plan(qo, kvp, last, mode=_lib.MASK_CAUSAL)
     assert p.shared_kv_tiles != 2
     qo5 = np.arange(B + 1, dtype=np.int32) * 5
     p, _ = _plan(qo5, kvp, last, mode=_lib.MASK_STREAMING, sink=64, window=512)
     assert p.shared_kv_tiles != 2
+    # the time model: 16 single-token requests (128 pairs) of 32-tile views favour the
+    # split (the longest view's run per wave, 4 tiles, against 2 MB per compute unit);
+    # 4-token drafts over the same views (16 rows per kv head: partials to merge) and
+    # 10-tile views favour the wave split
+    def views(n, tiles, q):
+        kv = np.full(n, 32 * tiles, np.int64)
+        return (np.arange(n + 1, dtype=np.int32) * q,
+                np.concatenate([[0], np.cumsum(kv // 16)]).astype(np.int32), np.full(n, 16, np.int32))
+    p, _ = _plan(*views(16, 32, 1))
+    assert p.shared_kv_tiles != 2
+    p, _ = _plan(*views(16, 32, 4))
+    assert p.shared_kv_tiles == 2
+    p, _ = _plan(*views(16, 10, 1))
+    assert p.shared_kv_tiles == 2

@@ -68,13 +68,13 @@ def test_device_shape_layout(B, hq, hkv, d, max_qo, mode):
                                               L["off_part"], L["off_dyn"], L["ints"])
     assert plan.off_merge_seqs % 4 == 0 and plan.num_split_requests == B
     # the same workgroup shape as a host plan whose longest request has max_qo tokens (on
-    # more compute units than (request, kv head) pairs: the host-only wave-split kernel,
-    # which a device plan never takes, needs the pairs to fill the device; the shape
-    # compared does not depend on the unit count)
+    # more than twice as many compute units as (request, kv head) pairs: the host-only
+    # wave-split kernel, which a device plan never takes, needs at least half the units
+    # in pairs; the shape compared does not depend on the unit count)
     qo = np.arange(B + 1, dtype=np.int32) * max_qo
     kvp = np.arange(B + 1, dtype=np.int32) * 4
     last = np.full(B, 16, np.int32)
-    cus = B * hkv + 1
+    cus = 2 * B * hkv + 1
     bound = int(lib.bsx_attn_plan_ints_bound(B, cus))
     blob = np.empty(bound, np.int32)
     hp = _lib.AttnPlan()
