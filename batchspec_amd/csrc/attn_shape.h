@@ -44,8 +44,9 @@ constexpr int kSplitMaxTiles = 4 * kSplitWaves;
 // Time model of the two schedules in microseconds, fitted on MI355X to the measured
 // kernel times (head dim 128, bf16) of decode and 4-token draft batches with 128..512
 // (request, kv head) pairs and views of 10..32 tiles; MB = visible K/V bytes / 1e6.
-//   wave-split: max(kWsLatencyUs + kWsWaveTileUs * (longest view's tiles) / kSplitWaves,
-//                   kWsFixedUs + kWsUsPerMB * MB)
+// Checked at head dim 64 and at 8 query heads per kv head (128..256 pairs).
+//   wave-split: max(kWsLatencyUs + kWsWaveTileUs * (D / 128) * (longest view's tiles)
+//                   / kSplitWaves, kWsFixedUs + kWsUsPerMB * MB)
 //     the longest view's run per wave, or the workgroups' streaming (5.5 TB/s)
 //   split-KV:   kSkFixedUs + kSkUsPerMB * MB + kSkRowUs * (query rows per kv head - 4)
 //     the merge launch and partials, the balanced stream (7.0 TB/s), the partial rows

@@ -343,7 +343,9 @@ static bool wave_split_fits(const HostSchedule& hs, const GridShape& gs, int bat
     }
   }
   const double mb = (double)tiles * num_kv_heads * as::head_tile_bytes(head_dim) * 1e-6;
-  const double ws_us = std::max(as::kWsLatencyUs + as::kWsWaveTileUs * longest / as::kSplitWaves,
+  // a wave's tile time scales with the head dim (its bytes and its matrix products)
+  const double wave_tile_us = as::kWsWaveTileUs * head_dim / 128.0;
+  const double ws_us = std::max(as::kWsLatencyUs + wave_tile_us * longest / as::kSplitWaves,
                                 as::kWsFixedUs + as::kWsUsPerMB * mb);
   const double sk_us = as::kSkFixedUs + as::kSkUsPerMB * mb +
                        as::kSkRowUs * std::max(0, hs.max_qo * group - 4);
