@@ -221,3 +221,16 @@ def test_captured_run_replays():
         want = w.run(q, cache)
         torch.cuda.synchronize()
         assert torch.equal(out, want), f"replay {rep} differs from the eager run"
+
+
+@pytest.mark.parametrize("qo", [1, 4])
+def test_head_dim_64_long_views(qo):
+    """Head dim 64 over views of up to 32 tiles (four per wave): the planner gives them to
+    the wave split at 128..256 pairs, single tokens and 4-token drafts alike."""
+    say(f"wave split: head dim 64, views of up to 32 tiles, {qo} query tokens")
+    for B, seed in ((16, 60 + qo), (32, 70 + qo)):
+        b = make_verify_batch(B, 30, 1000, qo, 32, 8, 64, 16, dtype=torch.bfloat16,
+                              seed=seed).to(DEV)
+        w = _plan(b, causal=True)
+        _assert_wave_split(w)
+        _check(b, w, "causal")
